@@ -1,0 +1,166 @@
+"""Host entry point of the MI355X sparse-MLA forward.
+
+Mirrors the reference's public operator ``dsa.forward`` (dsa/api.py:76-132):
+same positional arguments, tensor contract, return triple and exception types,
+with the device requirement moved from Ascend ("npu") to a ROCm GPU.  The work
+is one main-kernel launch plus, when the plan splits the KV range, one FP32
+merge launch, both enqueued through the C ABI on the current stream.  There
+is no CPU or fallback path.
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib
+from .config import Tuning, check_tuning, select
+
+HEAD_DIM = 512
+ROPE_DIM = 64
+SCALE = 1.0 / 24.0  # 576 ** -0.5, fixed by the operator contract (README.md:81-83 of the reference)
+_LDS_BYTES = 2 * 64 * 1152 + 2048 * 4
+
+
+@dataclass(frozen=True)
+class Launch:
+    """Descriptor of one kernel launch of a call (``return_kernels=True``)."""
+
+    name: str
+    grid: int
+    block: int
+    lds_bytes: int
+
+
+def _check_inputs(q, kv, q_rope, k_rope, indices):
+    """Shape, device, layout and dtype contract (reference: dsa/api.py:18-38).
+
+    Checks run in the reference's order (shapes, then device/contiguity, then
+    dtypes) and raise ValueError; index values are never read.
+    """
+    q_shape, kv_shape, ids_shape = tuple(q.shape), tuple(kv.shape), tuple(indices.shape)
+    if len(q_shape) != 4 or len(kv_shape) != 4 or len(ids_shape) != 4:
+        raise ValueError("q, kv and indices must be 4-D tensors")
+    batch, queries, heads, width = q_shape
+    length, topk = kv_shape[1], ids_shape[-1]
+    if (width != HEAD_DIM or kv_shape != (batch, length, 1, HEAD_DIM)
+            or tuple(q_rope.shape) != (batch, queries, heads, ROPE_DIM)
+            or tuple(k_rope.shape) != (batch, length, 1, ROPE_DIM)
+            or ids_shape != (batch, queries, 1, topk)
+            or min(batch, queries, heads, length, topk) <= 0):
+        raise ValueError("expected q[B,SQ,H,512], kv[B,L,1,512], q_rope[B,SQ,H,64], "
+                         "k_rope[B,L,1,64], indices[B,SQ,1,K]")
+    if heads % 16:
+        raise ValueError(f"the number of heads must be a multiple of 16 (got {heads})")
+    device = q.device
+    if (device.type != "cuda" or torch.version.hip is None
+            or any(t.device != device for t in (kv, q_rope, k_rope, indices))
+            or not all(t.is_contiguous() for t in (q, kv, q_rope, k_rope, indices))):
+        raise ValueError("all inputs must be contiguous and on the same ROCm GPU")
+    bf16 = torch.bfloat16
+    if (q.dtype != bf16 or kv.dtype != bf16 or q_rope.dtype != bf16 or k_rope.dtype != bf16
+            or indices.dtype != torch.int32):
+        raise ValueError("q/kv/q_rope/k_rope must be bfloat16 and indices int32")
+    return (batch, queries, heads, length, topk), device
+
+
+def plan_call(shape, config=None, cores: int = 256):
+    """Plan of one call: (Tuning, partial-buffer shapes or None, launches).
+
+    Pure host logic (reference: dsa/api.py:88-113); usable without a GPU.
+    """
+    if type(cores) is not int or cores <= 0:
+        raise ValueError("cores must be a positive int")
+    if config is None:
+        config = select(shape, cores)
+    else:
+        check_tuning(config, shape)
+    batch, queries, heads, _, _ = shape
+    tokens = batch * queries
+    launches = [Launch(f"sparse_mla_fwd_h{config.bm}_kw{config.kv_waves}_bn{config.bn}_s{config.stages}",
+                       tokens * config.split * (heads // config.bm), 256, _LDS_BYTES)]
+    partials = None
+    if config.split > 1:
+        partials = ((batch, queries, config.split, heads, HEAD_DIM), (batch, queries, config.split, heads))
+        launches.append(Launch("merge_partials", tokens * ((heads + 1) // 2), 256, 0))
+    return config, partials, tuple(launches)
+
+
+def forward(q, kv, q_rope, k_rope, indices, *, config=None, cores=None, return_kernels=False):
+    """Sparse MLA attention over given top-k indices.
+
+    Returns ``(output, softmax_max, softmax_sum)``: bf16 ``[B,SQ,H,512]`` and
+    two fp32 ``[B,1,SQ,H]`` tensors (max and sum of exp(score - max), not LSE).
+    The scale is fixed at 1/24.  Duplicate indices keep their weight; indices
+    outside ``[0, L)`` are masked; every query needs at least one valid index.
+
+    ``config``: a :class:`dsa_amd.Tuning` (default: the shape's table entry or
+    the library planner).  ``cores``: CU budget for planning (default: the
+    device's CU count).  ``return_kernels=True`` also returns the launch
+    descriptors.  Outputs are fresh tensors; nothing is cached across calls and
+    the call does not synchronise.
+    """
+    shape, device = _check_inputs(q, kv, q_rope, k_rope, indices)
+    if cores is None:
+        cores = torch.cuda.get_device_properties(device).multi_processor_count
+    config, partials, launches = plan_call(shape, config, cores)
+    batch, queries, heads, length, topk = shape
+
+    output = torch.empty_like(q)
+    maximum = torch.empty((batch, 1, queries, heads), device=device, dtype=torch.float32)
+    denominator = torch.empty_like(maximum)
+    if partials is None:
+        part_o = part_m = part_l = None
+    else:
+        part_o = torch.empty(partials[0], device=device, dtype=torch.float32)
+        part_m = torch.empty(partials[1], device=device, dtype=torch.float32)
+        part_l = torch.empty_like(part_m)
+
+    def ptr(t):
+        return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+    plan = config.to_c()
+    stream = torch.cuda.current_stream(device).cuda_stream
+    with torch.cuda.device(device):
+        rc = _lib.load().dsa_fwd(
+            ptr(q), ptr(kv), ptr(q_rope), ptr(k_rope), ptr(indices),
+            ptr(output), ptr(maximum), ptr(denominator), ptr(part_o), ptr(part_m), ptr(part_l),
+            batch, queries, heads, length, topk, ctypes.byref(plan), ctypes.c_void_p(stream))
+    _lib.check(rc, "dsa_fwd")
+    result = (output, maximum, denominator)
+    if return_kernels:
+        return result, launches
+    return result
+
+
+def merge(part_o, part_m, part_l):
+    """FP32 merge of split partials (reference: dsa/merge.py:13-91).
+
+    ``part_o [B,SQ,S,H,512]``, ``part_m``/``part_l [B,SQ,S,H]`` fp32 on one ROCm
+    GPU; returns ``(output, softmax_max, softmax_sum)`` as :func:`forward`.
+    """
+    if part_o.dim() != 5 or part_o.shape[-1] != HEAD_DIM:
+        raise ValueError("part_o must be [B,SQ,S,H,512]")
+    batch, queries, split, heads, _ = part_o.shape
+    for t in (part_m, part_l):
+        if tuple(t.shape) != (batch, queries, split, heads):
+            raise ValueError("part_m/part_l must be [B,SQ,S,H]")
+    device = part_o.device
+    if (device.type != "cuda" or any(t.device != device for t in (part_m, part_l))
+            or not all(t.is_contiguous() for t in (part_o, part_m, part_l))):
+        raise ValueError("partials must be contiguous and on the same ROCm GPU")
+    if any(t.dtype != torch.float32 for t in (part_o, part_m, part_l)):
+        raise ValueError("partials must be float32")
+    output = torch.empty((batch, queries, heads, HEAD_DIM), device=device, dtype=torch.bfloat16)
+    maximum = torch.empty((batch, 1, queries, heads), device=device, dtype=torch.float32)
+    denominator = torch.empty_like(maximum)
+    stream = torch.cuda.current_stream(device).cuda_stream
+    with torch.cuda.device(device):
+        rc = _lib.load().dsa_merge(
+            ctypes.c_void_p(part_o.data_ptr()), ctypes.c_void_p(part_m.data_ptr()),
+            ctypes.c_void_p(part_l.data_ptr()), ctypes.c_void_p(output.data_ptr()),
+            ctypes.c_void_p(maximum.data_ptr()), ctypes.c_void_p(denominator.data_ptr()),
+            batch * queries, heads, split, ctypes.c_void_p(stream))
+    _lib.check(rc, "dsa_merge")
+    return output, maximum, denominator

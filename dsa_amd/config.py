@@ -1,0 +1,133 @@
+"""Launch plans and the shape table of the MI355X sparse-MLA forward.
+
+Replaces dsa/config.py of the reference (Tuning :10-19, CASE_SHAPES :23-40,
+SELECTED :42-59, select :64-69).  The reference's Tuning fields described an
+Ascend Cube/Vector pipeline; here the plan describes gfx950 workgroups:
+
+* ``bm``       -- query heads per workgroup (16, 32 or 64; divides H);
+* ``bn``       -- gathered rows per LDS ring stage (64);
+* ``split``    -- KV splits per (token, head group); > 1 adds the FP32 merge;
+* ``kv_waves`` -- waves that share a head slice and split each tile's rows
+                  (``bm // 16 * kv_waves == 4``: four waves per workgroup);
+* ``stages``   -- LDS ring depth (2).
+
+Unlike the reference, shapes outside the table are accepted: the library's
+planner (``dsa_plan_for``) derives a plan for any supported shape.
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+
+from . import _lib
+
+
+@dataclass(frozen=True)
+class Tuning:
+    """Compile-time schedule of one call; never changes the math."""
+
+    bm: int
+    bn: int
+    split: int
+    kv_waves: int = 1
+    stages: int = 2
+
+    def to_c(self) -> _lib.DsaPlan:
+        p = _lib.DsaPlan()
+        p.heads_per_group, p.tile_rows, p.split = self.bm, self.bn, self.split
+        p.kv_waves, p.stages = self.kv_waves, self.stages
+        return p
+
+    @staticmethod
+    def from_c(p: _lib.DsaPlan) -> "Tuning":
+        return Tuning(p.heads_per_group, p.tile_rows, p.split, p.kv_waves, p.stages)
+
+
+# (batch, query length, heads, KV length, number of selected indices).
+# The reference's 16 cases (dsa/config.py:23-40) plus the five MI355X
+# benchmark configurations.
+CASE_SHAPES = {
+    "decode_b1": (1, 1, 128, 8192, 2048),
+    "decode_b8": (8, 1, 128, 32768, 2048),
+    "decode_b32": (32, 1, 128, 32768, 2048),
+    "decode_tp8": (8, 1, 16, 32768, 2048),
+    "prefill_q16": (1, 16, 128, 8192, 2048),
+    "prefill_q64": (1, 64, 128, 32768, 2048),
+    "prefill_tp8": (1, 128, 16, 32768, 2048),
+    "prefill_k512": (1, 128, 64, 32768, 512),
+    "decode_b4_h128": (4, 1, 128, 8192, 2048),
+    "prefill_b4_h128": (4, 8192, 128, 8192, 2048),
+    "decode_b4_h64": (4, 1, 64, 8192, 2048),
+    "prefill_b4_h64": (4, 8192, 64, 8192, 2048),
+    "decode_b4_h32": (4, 1, 32, 8192, 2048),
+    "prefill_b4_h32": (4, 8192, 32, 8192, 2048),
+    "decode_b4_h16": (4, 1, 16, 8192, 2048),
+    "prefill_b4_h16": (4, 8192, 16, 8192, 2048),
+    # MI355X benchmark configurations C1..C5
+    "c1_decode_b1": (1, 1, 128, 8192, 2048),
+    "c2_decode_b8": (8, 1, 128, 32768, 2048),
+    "c3_decode_h16_mtp": (64, 2, 16, 65536, 2048),
+    "c4_prefill_h16": (1, 4096, 16, 8192, 2048),
+    "c5_prefill_h128": (1, 4096, 128, 32768, 2048),
+}
+
+MI355X_CUS = 256
+
+
+def plan_for(shape, num_cus: int = MI355X_CUS) -> Tuning:
+    """Default plan the library derives for ``shape`` on ``num_cus`` CUs."""
+    b, sq, h, length, topk = shape
+    out = _lib.DsaPlan()
+    _lib.check(_lib.load().dsa_plan_for(b, sq, h, length, topk, num_cus, ctypes.byref(out)),
+               "dsa_plan_for")
+    return Tuning.from_c(out)
+
+
+def check_tuning(config: Tuning, shape) -> None:
+    """Validate a caller-supplied plan (reference: dsa/api.py:41-60)."""
+    if not isinstance(config, Tuning):
+        raise TypeError("config must be a dsa_amd.Tuning")
+    if any(type(v) is not int for v in (config.bm, config.bn, config.split, config.kv_waves, config.stages)):
+        raise ValueError("Tuning fields must be int")
+    b, sq, h, length, topk = shape
+    plan = config.to_c()
+    _lib.check(_lib.load().dsa_plan_check(ctypes.byref(plan), b, sq, h, length, topk), "invalid Tuning")
+
+
+# Per-shape plans for MI355X (256 CUs), re-derived from the reference's table
+# (dsa/config.py:42-59) for gfx950: four waves per workgroup, one 152 KiB
+# workgroup per CU, KV split until the grid covers the CUs.
+SELECTED = {
+    "decode_b1": Tuning(64, 64, 32),
+    "decode_b8": Tuning(64, 64, 16),
+    "decode_b32": Tuning(64, 64, 4),
+    "decode_tp8": Tuning(16, 64, 32, kv_waves=4),
+    "prefill_q16": Tuning(64, 64, 8),
+    "prefill_q64": Tuning(64, 64, 2),
+    "prefill_tp8": Tuning(16, 64, 2, kv_waves=4),
+    "prefill_k512": Tuning(64, 64, 2),
+    "decode_b4_h128": Tuning(64, 64, 32),
+    "prefill_b4_h128": Tuning(64, 64, 1),
+    "decode_b4_h64": Tuning(64, 64, 32),
+    "prefill_b4_h64": Tuning(64, 64, 1),
+    "decode_b4_h32": Tuning(32, 64, 32, kv_waves=2),
+    "prefill_b4_h32": Tuning(32, 64, 1, kv_waves=2),
+    "decode_b4_h16": Tuning(16, 64, 32, kv_waves=4),
+    "prefill_b4_h16": Tuning(16, 64, 1, kv_waves=4),
+    "c1_decode_b1": Tuning(64, 64, 32),
+    "c2_decode_b8": Tuning(64, 64, 16),
+    "c3_decode_h16_mtp": Tuning(16, 64, 2, kv_waves=4),
+    "c4_prefill_h16": Tuning(16, 64, 1, kv_waves=4),
+    "c5_prefill_h128": Tuning(64, 64, 1),
+}
+_BY_SHAPE = {}
+for _name, _shape in CASE_SHAPES.items():
+    _BY_SHAPE.setdefault(_shape, SELECTED[_name])
+
+
+def select(shape, num_cus: int = MI355X_CUS) -> Tuning:
+    """Plan for a shape: the table entry on a 256-CU device, else the planner's."""
+    shape = tuple(shape)
+    if num_cus == MI355X_CUS and shape in _BY_SHAPE:
+        return _BY_SHAPE[shape]
+    return plan_for(shape, num_cus)

@@ -1,0 +1,179 @@
+// C ABI of the library (include/dsa_mi355x.h): argument checks, launch
+// planning and the main + merge launch sequence of one forward call.
+//
+// Reference behaviour mirrored: dsa/api.py:18-38 (input contract),
+// dsa/api.py:41-60 (tuning checks), dsa/api.py:101-128 (allocation and the
+// main-kernel + merge launch pair).  The ABI never throws and never allocates.
+#include <hip/hip_runtime_api.h>
+
+#include <cstdarg>
+#include <cstdint>
+#include <cstdio>
+#include <cstring>
+
+#include "../../include/dsa_mi355x.h"
+#include "kernels.h"
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof g_err, fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+int hip_fail(int err, const char* what) {
+    return fail(err, "%s: %s (hipError_t %d)", what, hipGetErrorString((hipError_t)err), err);
+}
+
+constexpr int kTileRows = 64;
+constexpr int kStages = 2;
+
+int ceil_div(int a, int b) { return (a + b - 1) / b; }
+
+int check_shape(int B, int SQ, int H, int L, int TOPK) {
+    if (B <= 0 || SQ <= 0 || H <= 0 || L <= 0 || TOPK <= 0)
+        return fail(-1, "all of B, SQ, H, L, TOPK must be positive (got %d, %d, %d, %d, %d)", B, SQ, H, L, TOPK);
+    if (H % 16 != 0) return fail(-1, "H must be a multiple of 16 (got %d)", H);
+    if ((int64_t)B * SQ > (int64_t)1 << 30) return fail(-1, "B*SQ too large");
+    return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+int dsa_version(void) { return (1 << 16) | 0; }
+
+const char* dsa_last_error(void) { return g_err; }
+
+int dsa_plan_check(const dsa_plan* plan, int B, int SQ, int H, int L, int TOPK) {
+    if (!plan) return fail(-1, "plan is NULL");
+    if (int rc = check_shape(B, SQ, H, L, TOPK)) return rc;
+    const int hpg = plan->heads_per_group, bn = plan->tile_rows, split = plan->split;
+    if (hpg != 16 && hpg != 32 && hpg != 64)
+        return fail(-1, "heads_per_group must be 16, 32 or 64 (got %d)", hpg);
+    if (H % hpg) return fail(-1, "heads_per_group %d must divide H=%d", hpg, H);
+    if (bn != kTileRows) return fail(-1, "tile_rows must be %d (got %d)", kTileRows, bn);
+    if (plan->stages != kStages) return fail(-1, "stages must be %d (got %d)", kStages, plan->stages);
+    if (plan->kv_waves * (hpg / 16) != 4)
+        return fail(-1, "kv_waves * heads_per_group / 16 must be 4 (got kv_waves=%d)", plan->kv_waves);
+    if (!dsa::fwd_variant_exists(hpg, plan->kv_waves, bn, plan->stages))
+        return fail(-1, "no kernel variant for this plan");
+    const int ntiles = ceil_div(TOPK, bn);
+    if (split < 1 || split > ntiles)
+        return fail(-1, "split must be in [1, %d] for TOPK=%d (got %d)", ntiles, TOPK, split);
+    if (ceil_div(ntiles, split) * bn > DSA_IDX_CAP)
+        return fail(-1, "split %d leaves more than %d slots per workgroup (TOPK=%d)", split, DSA_IDX_CAP, TOPK);
+    g_err[0] = 0;
+    return 0;
+}
+
+int dsa_plan_for(int B, int SQ, int H, int L, int TOPK, int num_cus, dsa_plan* out) {
+    if (!out) return fail(-1, "out is NULL");
+    if (int rc = check_shape(B, SQ, H, L, TOPK)) return rc;
+    if (num_cus <= 0) return fail(-1, "num_cus must be positive (got %d)", num_cus);
+    dsa_plan p{};
+    // Four waves per workgroup: 64 heads x 1 row stream, 32 x 2 or 16 x 4.
+    p.heads_per_group = (H % 64 == 0) ? 64 : (H % 32 == 0) ? 32 : 16;
+    p.kv_waves = 4 / (p.heads_per_group / 16);
+    p.tile_rows = kTileRows;
+    p.stages = kStages;
+    // One 152 KiB workgroup fits a CU; split the KV range until the grid covers
+    // every CU once, but never below one tile per split.
+    const int ntiles = ceil_div(TOPK, kTileRows);
+    const int64_t base = (int64_t)B * SQ * (H / p.heads_per_group);
+    int split = 1;
+    if (base < num_cus) split = (int)((num_cus + base - 1) / base);
+    if (split > ntiles) split = ntiles;
+    const int min_split = ceil_div(ntiles * kTileRows, DSA_IDX_CAP);
+    if (split < min_split) split = min_split;
+    p.split = split;
+    *out = p;
+    return dsa_plan_check(out, B, SQ, H, L, TOPK);
+}
+
+int dsa_partial_elems(const dsa_plan* plan, int B, int SQ, int H, int64_t* part_o_elems,
+                      int64_t* part_ml_elems) {
+    if (!plan || !part_o_elems || !part_ml_elems) return fail(-1, "NULL argument");
+    if (B <= 0 || SQ <= 0 || H <= 0) return fail(-1, "B, SQ, H must be positive");
+    const int64_t rows = plan->split > 1 ? (int64_t)B * SQ * plan->split * H : 0;
+    *part_o_elems = rows * 512;
+    *part_ml_elems = rows;
+    g_err[0] = 0;
+    return 0;
+}
+
+int dsa_merge(const float* part_o, const float* part_m, const float* part_l, uint16_t* out, float* out_max,
+              float* out_sum, int tokens, int H, int split, hipStream_t stream) {
+    if (!part_o || !part_m || !part_l || !out || !out_max || !out_sum) return fail(-1, "NULL pointer argument");
+    if (tokens <= 0 || H <= 0 || split <= 0)
+        return fail(-1, "tokens, H, split must be positive (got %d, %d, %d)", tokens, H, split);
+    const int rc = dsa::launch_merge(part_o, part_m, part_l, out, out_max, out_sum, tokens, H, split, stream);
+    if (rc) return hip_fail(rc, "merge launch");
+    g_err[0] = 0;
+    return 0;
+}
+
+int dsa_fwd(const uint16_t* q, const uint16_t* kv, const uint16_t* q_rope, const uint16_t* k_rope,
+            const int32_t* idx, uint16_t* out, float* out_max, float* out_sum, float* part_o, float* part_m,
+            float* part_l, int B, int SQ, int H, int L, int TOPK, const dsa_plan* plan, hipStream_t stream) {
+    if (!q || !kv || !q_rope || !k_rope || !idx || !out || !out_max || !out_sum)
+        return fail(-1, "NULL input/output pointer");
+    if (int rc = check_shape(B, SQ, H, L, TOPK)) return rc;
+    dsa_plan local{};
+    if (!plan) {
+        int dev = 0, cus = 0;
+        int err = (int)hipGetDevice(&dev);
+        if (!err) err = (int)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+        if (err) return hip_fail(err, "querying the CU count");
+        if (int rc = dsa_plan_for(B, SQ, H, L, TOPK, cus, &local)) return rc;
+        plan = &local;
+    } else if (int rc = dsa_plan_check(plan, B, SQ, H, L, TOPK)) {
+        return rc;
+    }
+    if (plan->split > 1 && (!part_o || !part_m || !part_l))
+        return fail(-1, "split=%d needs part_o, part_m and part_l", plan->split);
+    // 16-byte vector accesses need 16-byte aligned rows.
+    if (((uintptr_t)q | (uintptr_t)kv | (uintptr_t)q_rope | (uintptr_t)k_rope | (uintptr_t)out) & 15)
+        return fail(-1, "q, kv, q_rope, k_rope and out must be 16-byte aligned");
+    if (plan->split > 1 && ((uintptr_t)part_o & 15)) return fail(-1, "part_o must be 16-byte aligned");
+
+    dsa::FwdParams p{};
+    p.q = q;
+    p.kv = kv;
+    p.q_rope = q_rope;
+    p.k_rope = k_rope;
+    p.idx = idx;
+    p.out = out;
+    p.out_max = out_max;
+    p.out_sum = out_sum;
+    p.part_o = part_o;
+    p.part_m = part_m;
+    p.part_l = part_l;
+    p.B = B;
+    p.SQ = SQ;
+    p.H = H;
+    p.L = L;
+    p.TOPK = TOPK;
+    p.nsplit = plan->split;
+    p.ntiles = ceil_div(TOPK, plan->tile_rows);
+    p.hgroups = H / plan->heads_per_group;
+    p.rowgroups = B * SQ * plan->split;
+    if (dsa::fwd_grid(p) > 0x7fffffff) return fail(-1, "grid too large");
+
+    int rc = dsa::launch_fwd(p, plan->heads_per_group, plan->kv_waves, plan->tile_rows, plan->stages, stream);
+    if (rc) return hip_fail(rc, "main kernel launch");
+    if (plan->split > 1) {
+        rc = dsa::launch_merge(part_o, part_m, part_l, out, out_max, out_sum, B * SQ, H, plan->split, stream);
+        if (rc) return hip_fail(rc, "merge launch");
+    }
+    g_err[0] = 0;
+    return 0;
+}
+
+}  // extern "C"

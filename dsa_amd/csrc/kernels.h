@@ -1,0 +1,47 @@
+// Internal interface between the C ABI (abi.cpp) and the gfx950 kernels
+// (sparse_mla_fwd.hip, merge.hip).  Not installed; the public surface is
+// include/dsa_mi355x.h.
+#pragma once
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+namespace dsa {
+
+// Everything one launch of the main kernel needs, passed by value as the
+// kernel argument block.
+struct FwdParams {
+    const uint16_t* q;       // [tokens, H, 512] bf16
+    const uint16_t* kv;      // [B, L, 512] bf16
+    const uint16_t* q_rope;  // [tokens, H, 64] bf16
+    const uint16_t* k_rope;  // [B, L, 64] bf16
+    const int32_t* idx;      // [tokens, TOPK] int32
+    uint16_t* out;           // [tokens, H, 512] bf16        (nsplit == 1)
+    float* out_max;          // [tokens, H]                  (nsplit == 1)
+    float* out_sum;          // [tokens, H]                  (nsplit == 1)
+    float* part_o;           // [tokens, nsplit, H, 512]     (nsplit > 1)
+    float* part_m;           // [tokens, nsplit, H]          (nsplit > 1)
+    float* part_l;           // [tokens, nsplit, H]          (nsplit > 1)
+    int B, SQ, H, L, TOPK;
+    int nsplit;              // KV splits per (token, head group)
+    int ntiles;              // ceil(TOPK / tile_rows)
+    int hgroups;             // H / heads_per_group
+    int rowgroups;           // tokens * nsplit
+};
+
+// Kernel variants compiled into the library, keyed by
+// (heads_per_group, kv_waves, tile_rows, stages).
+bool fwd_variant_exists(int heads_per_group, int kv_waves, int tile_rows, int stages);
+
+// Grid size (workgroups) of the main kernel for these params/plan.
+int64_t fwd_grid(const FwdParams& p);
+
+// Enqueue the main kernel; returns a hipError_t.
+int launch_fwd(const FwdParams& p, int heads_per_group, int kv_waves, int tile_rows,
+               int stages, hipStream_t stream);
+
+// Enqueue the split merge; returns a hipError_t.
+int launch_merge(const float* part_o, const float* part_m, const float* part_l,
+                 uint16_t* out, float* out_max, float* out_sum,
+                 int tokens, int H, int nsplit, hipStream_t stream);
+
+}  // namespace dsa

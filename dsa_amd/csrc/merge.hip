@@ -1,0 +1,68 @@
+// FP32 merge of split-KV partials (reference: dsa/merge.py:13-91, formula at
+// dsa/merge.py:1-5):
+//   m = max_s m_s;  w_s = exp(m_s - m);  l = sum_s w_s * l_s;
+//   out = bf16(sum_s w_s * u_s / l);  out_max = m;  out_sum = l.
+// One workgroup merges two heads of one token; each thread owns 4 of the 512
+// columns and streams the split partials with 16-byte loads.
+#include <hip/hip_runtime.h>
+#include <float.h>
+#include <stdint.h>
+
+#include "kernels.h"
+
+namespace dsa {
+namespace {
+
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;
+typedef __attribute__((__vector_size__(4 * sizeof(__bf16)))) __bf16 bf16x4;
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+__global__ __launch_bounds__(256) void merge_kernel(const float* __restrict__ part_o,
+                                                    const float* __restrict__ part_m,
+                                                    const float* __restrict__ part_l,
+                                                    uint16_t* __restrict__ out,
+                                                    float* __restrict__ out_max,
+                                                    float* __restrict__ out_sum, int H, int nsplit) {
+    const int pairs = (H + 1) >> 1;
+    const int token = blockIdx.x / pairs;
+    const int h = (blockIdx.x % pairs) * 2 + (threadIdx.x >> 7);
+    if (h >= H) return;
+    const int col = (threadIdx.x & 127) * 4;
+    const int64_t base = (int64_t)token * nsplit * H + h;  // + s * H
+
+    float m = -FLT_MAX;
+    for (int s = 0; s < nsplit; ++s) m = fmaxf(m, part_m[base + (int64_t)s * H]);
+    float l = 0.f;
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    for (int s = 0; s < nsplit; ++s) {
+        const int64_t row = base + (int64_t)s * H;
+        const float w = __builtin_amdgcn_exp2f((part_m[row] - m) * kLog2e);
+        l += w * part_l[row];
+        const f32x4 u = *reinterpret_cast<const f32x4*>(part_o + row * 512 + col);
+        acc += w * u;
+    }
+    bf16x4 o;
+    o[0] = (__bf16)(acc[0] / l);
+    o[1] = (__bf16)(acc[1] / l);
+    o[2] = (__bf16)(acc[2] / l);
+    o[3] = (__bf16)(acc[3] / l);
+    const int64_t orow = (int64_t)token * H + h;
+    *reinterpret_cast<bf16x4*>(out + orow * 512 + col) = o;
+    if ((threadIdx.x & 127) == 0) {
+        out_max[orow] = m;
+        out_sum[orow] = l;
+    }
+}
+
+}  // namespace
+
+int launch_merge(const float* part_o, const float* part_m, const float* part_l, uint16_t* out,
+                 float* out_max, float* out_sum, int tokens, int H, int nsplit, hipStream_t stream) {
+    const int64_t grid = (int64_t)tokens * ((H + 1) / 2);
+    hipLaunchKernelGGL(merge_kernel, dim3((unsigned)grid), dim3(256), 0, stream, part_o, part_m, part_l, out,
+                       out_max, out_sum, H, nsplit);
+    return (int)hipGetLastError();
+}
+
+}  // namespace dsa

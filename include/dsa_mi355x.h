@@ -1,0 +1,128 @@
+/*
+ * dsa_mi355x.h -- C ABI of the MI355X (gfx950) sparse-MLA attention forward.
+ *
+ * The library computes, for every token t = (b, s) and head h,
+ *
+ *   score_j = (q[t,h,:512] . kv[b,I_j,:] + q_rope[t,h,:64] . k_rope[b,I_j,:]) / 24
+ *   score_j = -inf  when I_j < 0 or I_j >= L            (index masked, slot kept)
+ *   max     = max_j score_j
+ *   sum     = sum_j exp(score_j - max)                  (FP32 exponentials)
+ *   out     = bf16( sum_j bf16(exp(score_j - max)) * kv[b,I_j,:] / sum )
+ *
+ * over the TOPK slots I_j = indices[t, j].  Duplicate slots keep their weight.
+ * Every row needs at least one valid slot (an all-invalid row returns NaN).
+ *
+ * Conventions of every entry point:
+ *   - plain pointers to device memory; bf16 tensors are passed as uint16_t
+ *     bit patterns; all tensors dense row-major (contiguous);
+ *   - the library allocates and frees nothing, and keeps no state across calls
+ *     other than read-only kernel handles;
+ *   - work is enqueued on `stream` (NULL = the default stream); no call
+ *     synchronises the device;
+ *   - return value: 0 = success, < 0 = invalid argument (nothing was enqueued),
+ *     > 0 = a hipError_t from the launch; dsa_last_error() then describes it.
+ *     No entry point throws.
+ *
+ * Reference interface replaced (CHNJZ/dsa):
+ *   dsa/api.py:76-132  forward()         -> dsa_plan_for + dsa_fwd (+ dsa_merge inside)
+ *   dsa/api.py:115-123 workspace_attention / ragged_attention launches -> main kernel of dsa_fwd
+ *   dsa/api.py:124-128 merge_partials launch (dsa/merge.py:13-91)     -> dsa_merge
+ *   dsa/config.py:10-19 Tuning, dsa/api.py:41-60 _check_tuning       -> dsa_plan, dsa_plan_check
+ */
+#ifndef DSA_MI355X_H
+#define DSA_MI355X_H
+
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define DSA_HEAD_DIM 512  /* latent (kv / value) width */
+#define DSA_ROPE_DIM 64   /* rotary part of the key */
+#define DSA_IDX_CAP 2048  /* max TOPK slots one workgroup handles (split >= ceil(TOPK/2048)) */
+
+/*
+ * Launch plan of one call.  Replaces dsa.Tuning (dsa/config.py:10-19), whose
+ * fields were Ascend-specific (BM, BN, split, direct_nz, pv_cols, share_score).
+ *
+ *   heads_per_group : query heads one workgroup owns (16, 32 or 64; divides H)
+ *   tile_rows       : gathered rows per LDS ring stage (64)
+ *   split           : KV splits per (token, head group); > 1 adds the FP32 merge
+ *   kv_waves        : waves that share a head slice and split each tile's rows
+ *                     (heads_per_group / 16 * kv_waves == 4)
+ *   stages          : LDS ring depth (2)
+ */
+typedef struct dsa_plan {
+    int32_t heads_per_group;
+    int32_t tile_rows;
+    int32_t split;
+    int32_t kv_waves;
+    int32_t stages;
+    int32_t reserved[3];
+} dsa_plan;
+
+/* Library version, (major << 16) | minor. */
+int dsa_version(void);
+
+/* Thread-local text of the last failure on this thread ("" if none). */
+const char* dsa_last_error(void);
+
+/*
+ * Default plan for a shape on a device with `num_cus` compute units.
+ * Replaces the shape-keyed table lookup of dsa/api.py:88-95 (_DEFAULT_CONFIGS),
+ * which rejected every shape outside its 16 entries; this covers any shape the
+ * kernels support.  Pure host logic: touches no device.
+ */
+int dsa_plan_for(int B, int SQ, int H, int L, int TOPK, int num_cus, dsa_plan* out);
+
+/*
+ * Validate a caller-supplied plan against a shape (dsa/api.py:41-60).
+ * Pure host logic.
+ */
+int dsa_plan_check(const dsa_plan* plan, int B, int SQ, int H, int L, int TOPK);
+
+/*
+ * Partial-buffer sizes (in float elements) a plan needs; 0 when split == 1.
+ * part_o: [B*SQ, split, H, 512]; part_m, part_l: [B*SQ, split, H].
+ * Mirrors the allocation at dsa/api.py:110-113.
+ */
+int dsa_partial_elems(const dsa_plan* plan, int B, int SQ, int H,
+                      int64_t* part_o_elems, int64_t* part_ml_elems);
+
+/*
+ * Sparse-MLA attention forward (dsa/api.py:76-132).
+ *
+ *   q      [B, SQ, H, 512] bf16     kv     [B, L, 1, 512] bf16
+ *   q_rope [B, SQ, H, 64]  bf16     k_rope [B, L, 1, 64]  bf16
+ *   idx    [B, SQ, 1, TOPK] int32
+ *   out    [B, SQ, H, 512] bf16     out_max, out_sum [B, 1, SQ, H] fp32
+ *   part_o, part_m, part_l: split partials (dsa_partial_elems); may be NULL when
+ *   plan->split == 1.  With split > 1 this enqueues the main kernel and then
+ *   the merge kernel on the same stream.
+ *   plan: NULL selects dsa_plan_for(..., device CU count).
+ */
+int dsa_fwd(const uint16_t* q, const uint16_t* kv, const uint16_t* q_rope,
+            const uint16_t* k_rope, const int32_t* idx,
+            uint16_t* out, float* out_max, float* out_sum,
+            float* part_o, float* part_m, float* part_l,
+            int B, int SQ, int H, int L, int TOPK,
+            const dsa_plan* plan, hipStream_t stream);
+
+/*
+ * FP32 merge of split partials (dsa/merge.py:13-91):
+ *   m = max_s m_s;  w_s = exp(m_s - m);  l = sum_s w_s l_s;
+ *   out = bf16(sum_s w_s u_s / l);  out_max = m;  out_sum = l.
+ *   part_o [tokens, split, H, 512], part_m/part_l [tokens, split, H] fp32.
+ * A split with (m_s = -FLT_MAX, l_s = 0, u_s = 0) carries weight 0.
+ */
+int dsa_merge(const float* part_o, const float* part_m, const float* part_l,
+              uint16_t* out, float* out_max, float* out_sum,
+              int tokens, int H, int split, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DSA_MI355X_H */

@@ -1,0 +1,201 @@
+"""CPU oracle of the sparse-MLA attention forward.
+
+TEST INFRASTRUCTURE ONLY.  Imported by ``tests/``, ``__graft_entry__.smoke()``
+and the ``cpu_baseline`` leg of ``bench.py`` -- as the checker, never as the
+thing measured or shipped.  The product path (``dsa_amd``) never imports it.
+
+Functions and the reference code each one restates:
+
+* ``reference``       -- the reference harness's FP32 oracle
+                         (tools/review.py:130-145): per batch and 16-query chunk,
+                         gather kv/k_rope rows in fp32, two bmm / 24, -inf mask
+                         from the raw index, amax / exp / sum, bmm(P / sum, kv).
+* ``accuracy``        -- its metrics (tools/review.py:146-175): max-normalised
+                         error N, relative RMS, per-row normalised error.
+* ``golden_stats``    -- the oracle statistics the reference's validation
+                         records hold (ref_max, ref_sq, elements).
+* ``online_softmax``  -- the tiled online-softmax recurrence
+                         (DSA从原理到实现.md:159-199; dsa/workspace.py:242-354).
+* ``merge_states``    -- the split-KV merge (dsa/merge.py:1-5, :56-87).
+* ``c_exact`` / ``c_tiled`` -- the C restatement in oracle/dsa_oracle.c:
+                         FP64 brute force, and the device-side arithmetic
+                         (tiles, bf16 P, FP32 state, split + merge).
+
+Pinning (tests/test_oracle.py): golden statistics of 20 reference validation
+records, both tutorial known-answer tests, reduction to a library
+scaled_dot_product_attention, FP64 brute force, closed forms of the uniform
+family, index-permutation / -1-removal / duplicate-counting invariants, and
+planted mistakes that each check must reject.
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+from pathlib import Path
+
+import numpy as np
+import torch
+
+SCALE_DIVISOR = 24.0  # score = dot / 24 (tools/review.py:140)
+HERE = Path(__file__).resolve().parent
+C_LIB = HERE / "_build" / "libdsa_oracle.so"
+
+
+def reference(q, kv, q_rope, k_rope, indices, chunk: int = 16, tokens=None):
+    """FP32 oracle: returns (output fp32 [B,SQ,H,512], max [B,1,SQ,H], sum [B,1,SQ,H]).
+
+    ``tokens``: optional iterable of (b, s) pairs; only those rows are computed
+    (the rest of the outputs stay NaN).
+    """
+    q, kv, q_rope, k_rope, indices = (t.cpu() for t in (q, kv, q_rope, k_rope, indices))
+    batch, queries, heads, _ = q.shape
+    length = kv.shape[1]
+    out = torch.full((batch, queries, heads, 512), float("nan"))
+    mx = torch.full((batch, 1, queries, heads), float("nan"))
+    sm = torch.full((batch, 1, queries, heads), float("nan"))
+    if tokens is None:
+        work = [(bi, list(range(s, min(queries, s + chunk))))
+                for bi in range(batch) for s in range(0, queries, chunk)]
+    else:
+        by_b: dict[int, list[int]] = {}
+        for bi, s in tokens:
+            by_b.setdefault(int(bi), []).append(int(s))
+        work = [(bi, ss[i:i + chunk]) for bi, ss in sorted(by_b.items()) for i in range(0, len(ss), chunk)]
+    for bi, rows in work:
+        rows_t = torch.tensor(rows)
+        index = indices[bi, rows_t, 0].long()
+        valid = (index >= 0) & (index < length)
+        index = index.clamp(0, length - 1)
+        selected = kv[bi, index, 0].float()
+        rope = k_rope[bi, index, 0].float()
+        score = (torch.bmm(q[bi, rows_t].float(), selected.transpose(1, 2))
+                 + torch.bmm(q_rope[bi, rows_t].float(), rope.transpose(1, 2))) / SCALE_DIVISOR
+        score.masked_fill_(~valid[:, None, :], -float("inf"))
+        maximum = score.amax(-1)
+        exponent = (score - maximum[..., None]).exp()
+        denominator = exponent.sum(-1)
+        out[bi, rows_t] = torch.bmm(exponent / denominator[..., None], selected)
+        mx[bi, 0, rows_t] = maximum
+        sm[bi, 0, rows_t] = denominator
+    return out, mx, sm
+
+
+def accuracy(actual, expected):
+    """Reference metrics (tools/review.py:146-175) of one output tensor pair."""
+    actual = actual.float().cpu()
+    expected = expected.float().cpu()
+    keep = ~torch.isnan(expected)
+    a, e = actual[keep], expected[keep]
+    delta = a - e
+    ref_max = float(e.abs().max())
+    return {
+        "max_abs": float(delta.abs().max()),
+        "reference_max": ref_max,
+        "max_normalized": float(delta.abs().max()) / max(ref_max, 1e-30),
+        "relative_rms": (float(delta.double().square().sum()) / max(float(e.double().square().sum()), 1e-30)) ** 0.5,
+        "finite": bool(torch.isfinite(a).all()),
+        "elements": int(e.numel()),
+    }
+
+
+def rel_error(actual, expected):
+    """max |actual - expected| / |expected| elementwise (for max/sum rtol gates)."""
+    actual = actual.double().cpu()
+    expected = expected.double().cpu()
+    keep = ~torch.isnan(expected)
+    return float(((actual[keep] - expected[keep]).abs() / expected[keep].abs().clamp_min(1e-30)).max())
+
+
+def golden_stats(out, mx, sm, chunk: int = 16):
+    """(reference_max, ref_sq, elements) per output, accumulated like the
+    reference harness: Python floats of fp32 per-(batch, chunk) sums."""
+    stats = {}
+    for key, t in (("output", out), ("maximum", mx), ("denominator", sm)):
+        t = t.float()
+        batch = t.shape[0]
+        queries = t.shape[1] if key == "output" else t.shape[2]
+        ref_sq, ref_max, n = 0.0, 0.0, 0
+        for bi in range(batch):
+            for s in range(0, queries, chunk):
+                piece = t[bi, s:s + chunk] if key == "output" else t[bi, 0, s:s + chunk]
+                ref_sq += float(piece.square().sum())
+                ref_max = max(ref_max, float(piece.abs().max()))
+                n += piece.numel()
+        stats[key] = {"reference_max": ref_max, "ref_sq": ref_sq, "elements": n}
+    return stats
+
+
+def online_softmax(scores, values, chunks):
+    """Scalar online softmax over ``chunks`` [(begin, end), ...] (float64).
+
+    Returns (m, l, u, u / l).  Restates DSA从原理到实现.md:181-197.
+    """
+    m, den, num = -math.inf, 0.0, 0.0
+    for begin, end in chunks:
+        nxt = max(m, max(scores[begin:end]))
+        rescale = math.exp(m - nxt) if m != -math.inf else 0.0
+        w = [math.exp(s - nxt) for s in scores[begin:end]]
+        den = rescale * den + sum(w)
+        num = rescale * num + sum(p * v for p, v in zip(w, values[begin:end]))
+        m = nxt
+    return m, den, num, num / den
+
+
+def merge_states(states):
+    """Merge split states [(m_s, l_s, u_s), ...] (dsa/merge.py:1-5) -> (m, l, u / l)."""
+    m = max(s[0] for s in states)
+    w = [math.exp(s[0] - m) for s in states]
+    den = sum(wi * s[1] for wi, s in zip(w, states))
+    num = sum(wi * s[2] for wi, s in zip(w, states))
+    return m, den, num / den
+
+
+# ------------------------------------------------------------------ C oracle
+_c = None
+
+
+def _c_lib():
+    global _c
+    if _c is None:
+        if not C_LIB.exists():
+            from . import build as _build  # noqa: F401  (oracle/build.py)
+            _build.build()
+        lib = ctypes.CDLL(str(C_LIB))
+        vp, i32 = ctypes.c_void_p, ctypes.c_int
+        for name, extra in (("dsa_oracle_exact", []), ("dsa_oracle_tiled", [i32, i32])):
+            fn = getattr(lib, name)
+            fn.restype = i32
+            fn.argtypes = [vp] * 5 + [i32] * 5 + extra + [vp] * 3
+        _c = lib
+    return _c
+
+
+def _bits(t):
+    return np.ascontiguousarray(t.cpu().contiguous().view(torch.int16).numpy())
+
+
+def _run_c(name, q, kv, q_rope, k_rope, indices, extra, dtype):
+    batch, queries, heads, _ = q.shape
+    length, topk = kv.shape[1], indices.shape[-1]
+    arrs = [_bits(q), _bits(kv), _bits(q_rope), _bits(k_rope),
+            np.ascontiguousarray(indices.cpu().int().numpy())]
+    out = np.zeros((batch, queries, heads, 512), dtype=dtype)
+    mx = np.zeros((batch, 1, queries, heads), dtype=dtype)
+    sm = np.zeros_like(mx)
+    ptrs = [ctypes.c_void_p(a.ctypes.data) for a in arrs + [out, mx, sm]]
+    rc = getattr(_c_lib(), name)(*ptrs[:5], batch, queries, heads, length, topk, *extra, *ptrs[5:])
+    if rc != 0:
+        raise ValueError(f"{name} rejected its arguments (rc={rc})")
+    return torch.from_numpy(out), torch.from_numpy(mx), torch.from_numpy(sm)
+
+
+def c_exact(q, kv, q_rope, k_rope, indices):
+    """FP64 brute force in C (float64 outputs)."""
+    return _run_c("dsa_oracle_exact", q, kv, q_rope, k_rope, indices, [], np.float64)
+
+
+def c_tiled(q, kv, q_rope, k_rope, indices, tile: int = 64, split: int = 1):
+    """Device-arithmetic model in C: FP32 tiles of ``tile`` slots, bf16 P,
+    ``split`` contiguous tile ranges merged in FP32.  Output is fp32 before the
+    final bf16 rounding."""
+    return _run_c("dsa_oracle_tiled", q, kv, q_rope, k_rope, indices, [tile, split], np.float32)

@@ -1,0 +1,82 @@
+"""The C-ABI library loads on the CPU and exports every symbol the header declares.
+
+No compute entry point is called with device memory here; only argument
+validation paths that return before any HIP call.
+"""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from dsa_amd import _lib
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "dsa_mi355x.h"
+
+
+def declared_functions():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(dsa_[a-z_]+)\s*\(", text)))
+
+
+def test_header_declares_the_expected_entry_points():
+    assert declared_functions() == sorted(
+        ["dsa_version", "dsa_last_error", "dsa_plan_for", "dsa_plan_check", "dsa_partial_elems",
+         "dsa_fwd", "dsa_merge"])
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    for name in declared_functions():
+        assert hasattr(lib, name), name
+        assert name in _lib.SIGNATURES, name
+
+
+def test_version_and_last_error():
+    lib = _lib.load()
+    assert lib.dsa_version() >> 16 == 1
+    assert isinstance(lib.dsa_last_error(), bytes)
+
+
+def test_struct_layout_matches_header():
+    assert ctypes.sizeof(_lib.DsaPlan) == 32
+
+
+def test_plan_for_rejects_bad_shapes():
+    lib = _lib.load()
+    plan = _lib.DsaPlan()
+    assert lib.dsa_plan_for(1, 1, 24, 10, 10, 256, ctypes.byref(plan)) < 0
+    assert b"multiple of 16" in lib.dsa_last_error()
+    assert lib.dsa_plan_for(0, 1, 16, 10, 10, 256, ctypes.byref(plan)) < 0
+    assert lib.dsa_plan_for(1, 1, 16, 10, 10, 0, ctypes.byref(plan)) < 0
+    assert lib.dsa_plan_for(1, 1, 16, 10, 10, 256, None) < 0
+    assert lib.dsa_plan_for(1, 1, 16, 10, 10, 256, ctypes.byref(plan)) == 0
+    assert lib.dsa_last_error() == b""
+
+
+def test_fwd_and_merge_validate_before_any_launch():
+    lib = _lib.load()
+    null = None
+    rc = lib.dsa_fwd(null, null, null, null, null, null, null, null, null, null, null,
+                     1, 1, 16, 10, 10, None, None)
+    assert rc < 0 and b"NULL" in lib.dsa_last_error()
+    rc = lib.dsa_merge(null, null, null, null, null, null, 1, 16, 2, None)
+    assert rc < 0
+
+
+def test_partial_elems():
+    lib = _lib.load()
+    plan = _lib.DsaPlan(64, 64, 4, 1, 2)
+    o, ml = ctypes.c_int64(), ctypes.c_int64()
+    assert lib.dsa_partial_elems(ctypes.byref(plan), 8, 1, 128, ctypes.byref(o), ctypes.byref(ml)) == 0
+    assert (o.value, ml.value) == (8 * 4 * 128 * 512, 8 * 4 * 128)
+    plan.split = 1
+    assert lib.dsa_partial_elems(ctypes.byref(plan), 8, 1, 128, ctypes.byref(o), ctypes.byref(ml)) == 0
+    assert (o.value, ml.value) == (0, 0)
+
+
+@pytest.mark.parametrize("split", [1, 3, 32])
+def test_plan_check_accepts_valid(split):
+    lib = _lib.load()
+    plan = _lib.DsaPlan(64, 64, split, 1, 2)
+    assert lib.dsa_plan_check(ctypes.byref(plan), 1, 1, 128, 8192, 2048) == 0

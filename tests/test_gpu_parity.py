@@ -1,0 +1,217 @@
+"""Parity of the gfx950 kernels (through dsa_amd.forward -> the C ABI) with the
+CPU oracle, on the reference's workloads and the MI355X benchmark configs.
+
+Tolerances: output max-normalised error
+max|out - ref| / max|ref| <= 1e-2 against the FP32 oracle; softmax_max and
+softmax_sum relative error <= 1e-4.  The reference's own kernels measured
+N <= 0.0036 on its records; values are printed for the log.
+"""
+import json
+from pathlib import Path
+
+import pytest
+import torch
+
+import dsa_amd
+from dsa_amd import Tuning
+from dsa_amd.workloads import baseline_inputs, review_inputs
+from oracle import dsa_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+OUT_TOL = 1e-2
+STAT_RTOL = 1e-4
+GOLDEN = json.loads((Path(__file__).parent / "golden" / "reference_stats.json").read_text())
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no ROCm GPU")
+    torch.cuda.init()
+
+
+def _report(tag, out, mx, sm, ref):
+    acc = O.accuracy(out, ref[0])
+    em, es = O.rel_error(mx, ref[1]), O.rel_error(sm, ref[2])
+    print(f"[{tag}] output N={acc['max_normalized']:.3e} rms={acc['relative_rms']:.3e} "
+          f"max rel={em:.2e} sum rel={es:.2e}", flush=True)
+    assert acc["finite"], tag
+    assert acc["max_normalized"] <= OUT_TOL, (tag, acc)
+    assert em <= STAT_RTOL, (tag, em)
+    assert es <= STAT_RTOL, (tag, es)
+    return acc
+
+
+def _run_and_check(tag, data, config=None, tokens=None):
+    print(f"[{tag}] launching shape={tuple(data[0].shape[:3])} L={data[1].shape[1]} "
+          f"K={data[4].shape[-1]} config={config}", flush=True)
+    out, mx, sm = dsa_amd.forward(*data, config=config)
+    torch.cuda.synchronize()
+    ref = O.reference(*[t.cpu() for t in data], tokens=tokens)
+    return _report(tag, out.cpu(), mx.cpu(), sm.cpu(), ref), (out, mx, sm)
+
+
+# ------------------------------------------------------- reference records
+RECORD_CASES = [r for r in GOLDEN["records"]
+                if r["shape"][0] * r["shape"][1] <= 128 and r["case"] not in ("decode_b32",)]
+
+
+@pytest.mark.parametrize("rec", RECORD_CASES, ids=lambda r: f"{r['case']}-{r['family']}-{r['source'].split('/')[1]}")
+def test_reference_records(rec):
+    data = tuple(t.cuda() for t in review_inputs(tuple(rec["shape"]), rec["seed"], rec["family"]))
+    acc, _ = _run_and_check(rec["case"] + "-" + rec["family"], data)
+    # the oracle run here reproduces the record's statistics
+    assert acc["reference_max"] == pytest.approx(rec["oracle"]["output"]["reference_max"], rel=1e-5)
+
+
+@pytest.mark.parametrize("family", ["uniform", "peaked", "duplicates", "invalid"])
+@pytest.mark.parametrize("case", ["decode_b1", "decode_tp8", "prefill_tp8"])
+def test_adversarial_families(case, family):
+    data = tuple(t.cuda() for t in review_inputs(dsa_amd.CASE_SHAPES[case], 20261103, family))
+    _run_and_check(f"{case}-{family}", data)
+
+
+def test_uniform_closed_form_on_device():
+    q, kv, qr, kr, ids = (t.cuda() for t in review_inputs((1, 1, 128, 8192, 2048), 20261103, "uniform"))
+    out, mx, sm = dsa_amd.forward(q, kv, qr, kr, ids)
+    assert torch.all(mx == 0)
+    assert torch.all(sm == 2048)
+
+
+# ------------------------------------------------------- MI355X configs C1..C5
+def test_c1_full():
+    data = baseline_inputs("c1_decode_b1")
+    _run_and_check("c1", data)
+
+
+def test_c2_full():
+    data = baseline_inputs("c2_decode_b8")
+    _run_and_check("c2", data)
+
+
+def _subset(name, picks):
+    data = baseline_inputs(name)
+    batch, queries = data[0].shape[:2]
+    tokens = [(b, s) for b, s in picks if b < batch and s < queries]
+    return data, tokens
+
+
+def test_c3_sampled_tokens():
+    data, tokens = _subset("c3_decode_h16_mtp", [(b, s) for b in (0, 1, 17, 40, 63) for s in (0, 1)])
+    _run_and_check("c3", data, tokens=tokens)
+
+
+def test_c4_sampled_tokens():
+    data, tokens = _subset("c4_prefill_h16", [(0, s) for s in (0, 1, 2, 777, 2048, 3000, 4094, 4095)])
+    _run_and_check("c4", data, tokens=tokens)
+
+
+def test_c5_sampled_tokens_per_family():
+    picks = [(0, f * 1024 + s) for f in range(4) for s in (0, 1, 511, 1023)]
+    data, tokens = _subset("c5_prefill_h128", picks)
+    _run_and_check("c5", data, tokens=tokens)
+
+
+# ------------------------------------------------------- plans, edges, invariants
+PLANS_H128 = [Tuning(64, 64, 1), Tuning(64, 64, 2), Tuning(64, 64, 7), Tuning(64, 64, 32),
+              Tuning(32, 64, 1, kv_waves=2), Tuning(32, 64, 5, kv_waves=2),
+              Tuning(16, 64, 1, kv_waves=4), Tuning(16, 64, 32, kv_waves=4)]
+
+
+@pytest.mark.parametrize("config", PLANS_H128, ids=str)
+def test_every_variant_and_split(config):
+    data = tuple(t.cuda() for t in review_inputs((2, 2, 128, 4096, 2048), 7, "invalid"))
+    _run_and_check(f"plan-{config}", data, config=config)
+
+
+def _random_case(seed, B, SQ, H, L, K, invalid=0.1, dup=0.1):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(B, SQ, H, 512, generator=g).bfloat16()
+    kv = torch.randn(B, L, 1, 512, generator=g).bfloat16()
+    qr = torch.randn(B, SQ, H, 64, generator=g).bfloat16()
+    kr = torch.randn(B, L, 1, 64, generator=g).bfloat16()
+    ids = torch.randint(0, L, (B, SQ, 1, K), generator=g, dtype=torch.int32)
+    u = torch.rand(ids.shape, generator=g)
+    ids[u < invalid / 2] = -1
+    ids[(u >= invalid / 2) & (u < invalid)] = L + 5 + (u[(u >= invalid / 2) & (u < invalid)] * 1000).int()
+    ids[..., :1] = torch.randint(0, L, (B, SQ, 1, 1), generator=g, dtype=torch.int32)
+    d = torch.rand(ids.shape, generator=g) < dup
+    ids[..., 1:][d[..., 1:]] = ids[..., :-1][d[..., 1:]]
+    return tuple(t.cuda() for t in (q, kv, qr, kr, ids.contiguous()))
+
+
+@pytest.mark.parametrize("B,SQ,H,L,K", [
+    (1, 1, 16, 1, 1),          # one row, one slot
+    (1, 1, 16, 5, 70),         # TOPK > L: heavy duplication, ragged last tile
+    (2, 3, 48, 1000, 100),     # H = 3 x 16, ragged TOPK
+    (1, 2, 32, 3000, 2047),    # ragged by one
+    (3, 1, 80, 20000, 4096),   # H = 5 x 16, TOPK 4096 (split >= 2 forced)
+    (1, 1, 64, 70000, 8192),   # TOPK 8192, index cache forces split >= 4
+])
+def test_edge_shapes(B, SQ, H, L, K):
+    data = _random_case(B * 1000 + K, B, SQ, H, L, K)
+    _run_and_check(f"edge-{B}x{SQ}x{H}x{L}x{K}", data)
+
+
+def test_all_slots_twice_doubles_sum():
+    data = _random_case(11, 2, 2, 64, 5000, 1024, invalid=0.0, dup=0.0)
+    out, mx, sm = dsa_amd.forward(*data)
+    twice = torch.cat([data[4], data[4]], dim=-1).contiguous()
+    out2, mx2, sm2 = dsa_amd.forward(*data[:4], twice)
+    assert O.accuracy(out2.cpu(), out.float().cpu())["max_normalized"] < 1e-2
+    assert torch.equal(mx, mx2)
+    torch.testing.assert_close(sm2, 2 * sm, rtol=1e-5, atol=0)
+
+
+def test_deterministic_bitwise():
+    data = baseline_inputs("c2_decode_b8")
+    a = dsa_amd.forward(*data)
+    b = dsa_amd.forward(*data)
+    torch.cuda.synchronize()
+    assert torch.equal(a[0].view(torch.int16), b[0].view(torch.int16))
+    assert torch.equal(a[1].view(torch.int32), b[1].view(torch.int32))
+    assert torch.equal(a[2].view(torch.int32), b[2].view(torch.int32))
+
+
+def test_side_stream():
+    data = _random_case(12, 2, 1, 128, 4096, 2048)
+    ref = dsa_amd.forward(*data)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        got = dsa_amd.forward(*data)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    assert torch.equal(ref[0], got[0])
+
+
+def test_standalone_merge_matches_oracle():
+    g = torch.Generator().manual_seed(3)
+    B, SQ, S, H = 2, 3, 5, 32
+    part_o = torch.randn(B, SQ, S, H, 512, generator=g)
+    part_m = torch.randn(B, SQ, S, H, generator=g) * 3
+    part_l = torch.rand(B, SQ, S, H, generator=g) * 10 + 0.5
+    part_m[0, 0, 1] = -3.4028234663852886e38  # an empty split
+    part_l[0, 0, 1] = 0.0
+    part_o[0, 0, 1] = 0.0
+    out, mx, sm = dsa_amd.merge(part_o.cuda(), part_m.cuda(), part_l.cuda())
+    torch.cuda.synchronize()
+    w = torch.exp(part_m.double() - part_m.double().amax(2, keepdim=True))
+    l_ref = (w * part_l.double()).sum(2)
+    o_ref = (w[..., None] * part_o.double()).sum(2) / l_ref[..., None]
+    torch.testing.assert_close(mx.cpu()[:, 0].double(), part_m.double().amax(2), rtol=0, atol=0)
+    torch.testing.assert_close(sm.cpu()[:, 0].double(), l_ref, rtol=1e-5, atol=0)
+    torch.testing.assert_close(out.cpu().double(), o_ref, rtol=8e-3, atol=1e-6)
+
+
+def test_dtype_and_contiguity_rejections_on_device():
+    data = _random_case(13, 1, 1, 16, 100, 64)
+    with pytest.raises(ValueError):
+        dsa_amd.forward(data[0].float(), *data[1:])
+    with pytest.raises(ValueError):
+        dsa_amd.forward(*data[:4], data[4].long())
+    q_nc = torch.empty(1, 1, 16, 1024, dtype=torch.bfloat16, device="cuda")[..., :512]
+    assert not q_nc.is_contiguous()
+    with pytest.raises(ValueError):
+        dsa_amd.forward(q_nc, *data[1:])

@@ -1,0 +1,144 @@
+"""Host contract of dsa_amd.forward without a GPU.
+
+Mirrors the reference's CPU-only host checks (tools/check_host_api.py:88-129):
+every rejection is raised before any allocation or launch, with the
+reference's exception types (ValueError for shapes/devices/dtypes/plans,
+TypeError for a config of the wrong type).  Planning runs in the C library,
+which loads and plans without touching a device.
+"""
+import pytest
+import torch
+
+import dsa_amd
+from dsa_amd import CASE_SHAPES, SELECTED, Tuning, plan_call
+from dsa_amd.api import _check_inputs
+from dsa_amd.config import check_tuning, plan_for
+from dsa_amd.workloads import BASELINE_CONFIGS
+
+
+def _tensors(B=2, SQ=3, H=16, L=40, K=24, device="cpu"):
+    return (torch.zeros(B, SQ, H, 512, dtype=torch.bfloat16, device=device),
+            torch.zeros(B, L, 1, 512, dtype=torch.bfloat16, device=device),
+            torch.zeros(B, SQ, H, 64, dtype=torch.bfloat16, device=device),
+            torch.zeros(B, L, 1, 64, dtype=torch.bfloat16, device=device),
+            torch.zeros(B, SQ, 1, K, dtype=torch.int32, device=device))
+
+
+SHAPE_MUTATIONS = {
+    "q rank": lambda t: (t[0][0],) + t[1:],
+    "kv rank": lambda t: (t[0], t[1][0]) + t[2:],
+    "ids rank": lambda t: t[:4] + (t[4][0],),
+    "q width": lambda t: (torch.zeros(2, 3, 16, 256, dtype=torch.bfloat16),) + t[1:],
+    "kv width": lambda t: (t[0], torch.zeros(2, 40, 1, 256, dtype=torch.bfloat16)) + t[2:],
+    "kv heads": lambda t: (t[0], torch.zeros(2, 40, 2, 512, dtype=torch.bfloat16)) + t[2:],
+    "kv batch": lambda t: (t[0], torch.zeros(3, 40, 1, 512, dtype=torch.bfloat16)) + t[2:],
+    "q_rope width": lambda t: t[:2] + (torch.zeros(2, 3, 16, 32, dtype=torch.bfloat16),) + t[3:],
+    "q_rope heads": lambda t: t[:2] + (torch.zeros(2, 3, 8, 64, dtype=torch.bfloat16),) + t[3:],
+    "k_rope length": lambda t: t[:3] + (torch.zeros(2, 41, 1, 64, dtype=torch.bfloat16),) + t[4:],
+    "ids queries": lambda t: t[:4] + (torch.zeros(2, 4, 1, 24, dtype=torch.int32),),
+    "ids heads": lambda t: t[:4] + (torch.zeros(2, 3, 2, 24, dtype=torch.int32),),
+    "zero length": lambda t: _tensors(L=0),
+    "zero topk": lambda t: _tensors(K=0),
+    "heads not multiple of 16": lambda t: _tensors(H=24),
+}
+
+
+@pytest.mark.parametrize("name", sorted(SHAPE_MUTATIONS))
+def test_shape_rejections(name):
+    bad = SHAPE_MUTATIONS[name](_tensors())
+    with pytest.raises(ValueError):
+        _check_inputs(*bad)
+    with pytest.raises(ValueError):
+        dsa_amd.forward(*bad)
+
+
+def test_cpu_tensors_rejected_as_device_error():
+    with pytest.raises(ValueError, match="ROCm GPU"):
+        dsa_amd.forward(*_tensors())
+
+
+def test_meta_tensors_rejected():
+    with pytest.raises(ValueError, match="ROCm GPU"):
+        dsa_amd.forward(*_tensors(device="meta"))
+
+
+def test_exports_match_reference_surface():
+    for name in ("forward", "Tuning", "CASE_SHAPES", "SELECTED"):
+        assert hasattr(dsa_amd, name)
+    assert set(SELECTED) == set(CASE_SHAPES)
+
+
+@pytest.mark.parametrize("name", sorted(CASE_SHAPES))
+def test_selected_plans_are_valid(name):
+    check_tuning(SELECTED[name], CASE_SHAPES[name])
+
+
+@pytest.mark.parametrize("name", sorted(BASELINE_CONFIGS))
+def test_baseline_configs_in_table(name):
+    assert CASE_SHAPES[name] == BASELINE_CONFIGS[name]
+    assert dsa_amd.select(CASE_SHAPES[name]) == SELECTED[name]
+
+
+@pytest.mark.parametrize("shape", [(1, 1, 16, 1, 1), (3, 5, 48, 1000, 777), (2, 7, 32, 9, 4097),
+                                   (1, 1, 128, 65536, 8192), (64, 2, 16, 65536, 2048)])
+def test_planner_covers_any_shape(shape):
+    plan = plan_for(shape)
+    check_tuning(plan, shape)
+    topk = shape[-1]
+    ntiles = -(-topk // plan.bn)
+    assert 1 <= plan.split <= ntiles
+    assert -(-ntiles // plan.split) * plan.bn <= 2048  # index cache of one workgroup
+    assert shape[2] % plan.bm == 0 and plan.bm // 16 * plan.kv_waves == 4
+
+
+def test_plan_call_allocations_and_launches():
+    shape = CASE_SHAPES["decode_b8"]
+    config, partials, launches = plan_call(shape, cores=256)
+    assert config == SELECTED["decode_b8"]
+    assert partials == ((8, 1, config.split, 128, 512), (8, 1, config.split, 128))
+    assert [l.name for l in launches] == [launches[0].name, "merge_partials"]
+    assert launches[0].grid == 8 * config.split * (128 // config.bm)
+    config, partials, launches = plan_call(CASE_SHAPES["c5_prefill_h128"], cores=256)
+    assert config.split == 1 and partials is None and len(launches) == 1
+
+
+def test_plan_call_explicit_tuning_and_errors():
+    shape = (1, 1, 128, 8192, 2048)
+    config, partials, _ = plan_call(shape, Tuning(32, 64, 4, kv_waves=2))
+    assert config.split == 4 and partials[0][2] == 4
+    with pytest.raises(ValueError):
+        plan_call(shape, cores=0)
+    with pytest.raises(ValueError):
+        plan_call(shape, cores=2.0)
+
+
+TUNING_MUTATIONS = {
+    "bm not dividing H": Tuning(64, 64, 1),
+    "bm 48": Tuning(48, 64, 1),
+    "bn 128": Tuning(16, 128, 1, kv_waves=4),
+    "split 0": Tuning(16, 64, 0, kv_waves=4),
+    "split > tiles": Tuning(16, 64, 2, kv_waves=4),
+    "kv_waves mismatch": Tuning(16, 64, 1, kv_waves=1),
+    "stages 3": Tuning(16, 64, 1, kv_waves=4, stages=3),
+}
+
+
+@pytest.mark.parametrize("name", sorted(TUNING_MUTATIONS))
+def test_tuning_rejections(name):
+    shape = (1, 1, 16, 100, 64)  # one tile of 64 slots
+    with pytest.raises(ValueError):
+        check_tuning(TUNING_MUTATIONS[name], shape)
+
+
+def test_tuning_type_error():
+    with pytest.raises(TypeError):
+        check_tuning((64, 64, 1), (1, 1, 64, 10, 10))
+    with pytest.raises(ValueError):
+        check_tuning(Tuning(64.0, 64, 1), (1, 1, 64, 10, 10))
+
+
+def test_index_cache_limit_forces_split():
+    # TOPK 8192 = 128 tiles; one workgroup holds at most 2048 slots -> split >= 4
+    with pytest.raises(ValueError):
+        check_tuning(Tuning(64, 64, 2), (1, 1, 64, 100000, 8192))
+    check_tuning(Tuning(64, 64, 4), (1, 1, 64, 100000, 8192))

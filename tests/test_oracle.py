@@ -1,0 +1,231 @@
+"""Pin the CPU oracle (oracle/dsa_oracle.py, oracle/dsa_oracle.c) before
+trusting it as the parity checker.
+
+* golden statistics of the reference's own FP32-oracle records
+  (tests/golden/reference_stats.json, from validation/*/result.json);
+* the tutorial known-answer tests (DSA从原理到实现.md:159-217);
+* reduction to torch's scaled_dot_product_attention / logsumexp;
+* FP64 brute force in C;
+* closed forms of the ``uniform`` family and index invariants;
+* planted mistakes in the oracle that these checks must reject.
+"""
+import json
+import math
+import os
+from pathlib import Path
+
+import pytest
+import torch
+
+from dsa_amd.workloads import review_inputs
+from oracle import dsa_oracle as O
+
+GOLDEN = json.loads((Path(__file__).parent / "golden" / "reference_stats.json").read_text())
+RECORDS = GOLDEN["records"]
+# CPU-feasible records.  The reference's four B=4 x 8192-query prefill cases
+# and decode_b32 take ~4 minutes together (and ~10 GB of fp32 temporaries);
+# they run when DSA_SLOW_TESTS=1.
+FAST = [r for r in RECORDS if r["shape"][0] * r["shape"][1] <= 128 and r["case"] != "decode_b32"]
+SLOW = [r for r in RECORDS if r not in FAST]
+REL = 1e-5
+
+
+def _rid(r):
+    return f"{r['case']}-{r['family']}-{r['seed']}-{r['source'].split('/')[1]}"
+
+
+def _check_record(rec):
+    shape = tuple(rec["shape"])
+    data = review_inputs(shape, rec["seed"], rec["family"])
+    got = O.golden_stats(*O.reference(*data))
+    for key, want in rec["oracle"].items():
+        assert got[key]["elements"] == want["elements"], key
+        for stat in ("reference_max", "ref_sq"):
+            assert got[key][stat] == pytest.approx(want[stat], rel=REL), (key, stat)
+
+
+@pytest.mark.parametrize("rec", FAST, ids=_rid)
+def test_golden_statistics(rec):
+    _check_record(rec)
+
+
+@pytest.mark.slow
+@pytest.mark.skipif(not os.environ.get("DSA_SLOW_TESTS"), reason="set DSA_SLOW_TESTS=1 (about 4 minutes)")
+@pytest.mark.parametrize("rec", SLOW, ids=_rid)
+def test_golden_statistics_large(rec):
+    _check_record(rec)
+
+
+def _record(case, family="normal"):
+    return next(r for r in RECORDS if r["case"] == case and r["family"] == family)
+
+
+# ------------------------------------------------------------ planted mistakes
+def _golden_fails(rec, monkeypatch, patch):
+    with monkeypatch.context() as mp:
+        patch(mp)
+        with pytest.raises(AssertionError):
+            _check_record(rec)
+
+
+def test_planted_wrong_scale_is_caught(monkeypatch):
+    # 1/sqrt(512) instead of 1/sqrt(576)
+    _golden_fails(_record("decode_b1"), monkeypatch,
+                  lambda mp: mp.setattr(O, "SCALE_DIVISOR", math.sqrt(512.0)))
+
+
+def test_planted_dropped_rope_is_caught(monkeypatch):
+    real = O.reference
+
+    def no_rope(q, kv, q_rope, k_rope, indices, **kw):
+        return real(q, kv, torch.zeros_like(q_rope), k_rope, indices, **kw)
+
+    _golden_fails(_record("decode_b1"), monkeypatch, lambda mp: mp.setattr(O, "reference", no_rope))
+
+
+def test_planted_unmasked_invalid_is_caught(monkeypatch):
+    real = O.reference
+
+    def clamp_instead_of_mask(q, kv, q_rope, k_rope, indices, **kw):
+        return real(q, kv, q_rope, k_rope, indices.clamp_min(0), **kw)
+
+    rec = next(r for r in RECORDS if r["family"] == "invalid" and r["case"] == "decode_b1")
+    _golden_fails(rec, monkeypatch, lambda mp: mp.setattr(O, "reference", clamp_instead_of_mask))
+
+
+def test_planted_deduplication_is_caught(monkeypatch):
+    real = O.reference
+
+    def dedup(q, kv, q_rope, k_rope, indices, **kw):
+        ids = indices.clone()
+        ids[..., 1::2] = -1  # the duplicates family repeats every even slot
+        return real(q, kv, q_rope, k_rope, ids, **kw)
+
+    rec = next(r for r in RECORDS if r["family"] == "duplicates" and r["case"] == "decode_b1")
+    _golden_fails(rec, monkeypatch, lambda mp: mp.setattr(O, "reference", dedup))
+
+
+# ------------------------------------------------------------ known answers
+def test_kat_online_softmax():
+    k = GOLDEN["kats"]["online_softmax"]
+    chunks = [tuple(c) for c in k["chunks"]]
+    m, l, u, o = O.online_softmax(k["scores"], k["values"], chunks)
+    assert o == pytest.approx(k["output"], rel=1e-14)
+    assert l == pytest.approx(k["l"], rel=1e-9)
+    assert u == pytest.approx(k["u"], rel=1e-9)
+    m1, l1, u1, _ = O.online_softmax(k["scores"], k["values"], chunks[:1])
+    assert [m1, l1, u1] == pytest.approx(k["state_after_first_chunk"], rel=1e-9)
+    # chunking never changes the result
+    for split in ([(0, 1), (1, 2), (2, 3)], [(0, 3)], [(0, 1), (1, 3)]):
+        assert O.online_softmax(k["scores"], k["values"], split)[3] == pytest.approx(k["output"], rel=1e-14)
+
+
+def test_kat_split_merge():
+    k = GOLDEN["kats"]["split_merge"]
+    m, l, o = O.merge_states([tuple(k["a"]), tuple(k["b"])])
+    assert o == pytest.approx(k["output"], rel=1e-9)
+    assert m == 3.0
+    naive = (k["a"][2] / k["a"][1] + k["b"][2] / k["b"][1]) / 2
+    assert naive == pytest.approx(k["wrong_average"], rel=1e-9)
+    assert abs(o - naive) > 1.0
+
+
+def test_merge_empty_split_has_zero_weight():
+    flt_max = 3.4028234663852886e38
+    m, l, o = O.merge_states([(-flt_max, 0.0, 0.0), (3.0, 1.0, 40.0)])
+    assert (m, l, o) == (3.0, 1.0, 40.0)
+
+
+# ------------------------------------------------------------ small random cases
+def _small(seed, batch=2, queries=3, heads=16, length=97, topk=45, invalid=0.2, dup=0.2):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(batch, queries, heads, 512, generator=g).bfloat16()
+    kv = torch.randn(batch, length, 1, 512, generator=g).bfloat16()
+    qr = torch.randn(batch, queries, heads, 64, generator=g).bfloat16()
+    kr = torch.randn(batch, length, 1, 64, generator=g).bfloat16()
+    ids = torch.randint(0, length, (batch, queries, 1, topk), generator=g, dtype=torch.int32)
+    u = torch.rand(ids.shape, generator=g)
+    ids[u < invalid] = -1
+    ids[(u > 1 - invalid / 2)] = length + 3  # out of range above
+    ids[..., 0] = torch.randint(0, length, (batch, queries, 1), generator=g, dtype=torch.int32)  # >= 1 valid
+    d = torch.rand(ids.shape, generator=g) < dup
+    ids[..., 1:][d[..., 1:]] = ids[..., :-1][d[..., 1:]]
+    return q, kv, qr, kr, ids
+
+
+@pytest.mark.parametrize("seed", [1, 2, 3])
+def test_matches_library_sdpa(seed):
+    q, kv, qr, kr, ids = _small(seed)
+    out, mx, sm = O.reference(q, kv, qr, kr, ids)
+    length = kv.shape[1]
+    for b in range(q.shape[0]):
+        for s in range(q.shape[1]):
+            idx = ids[b, s, 0].long()
+            valid = (idx >= 0) & (idx < length)
+            rows = kv[b, idx.clamp(0, length - 1), 0].double()
+            keys = torch.cat([rows, kr[b, idx.clamp(0, length - 1), 0].double()], dim=-1)
+            query = torch.cat([q[b, s].double(), qr[b, s].double()], dim=-1)
+            mask = valid[None, :].expand(q.shape[2], -1)
+            ref = torch.nn.functional.scaled_dot_product_attention(
+                query[None], keys[None], rows[None], attn_mask=mask[None], scale=1 / 24)[0]
+            torch.testing.assert_close(out[b, s].double(), ref, rtol=2e-5, atol=2e-6)
+            score = (query @ keys.T) / 24
+            score[~mask] = -float("inf")
+            lse = torch.logsumexp(score, -1)
+            torch.testing.assert_close(mx[b, 0, s].double() + sm[b, 0, s].double().log(), lse,
+                                       rtol=1e-6, atol=1e-6)
+
+
+@pytest.mark.parametrize("seed", [4, 5])
+def test_matches_c_fp64_brute_force(seed):
+    data = _small(seed)
+    out, mx, sm = O.reference(*data)
+    eo, em, es = O.c_exact(*data)
+    torch.testing.assert_close(out.double(), eo, rtol=1e-5, atol=1e-6)
+    torch.testing.assert_close(mx.double(), em, rtol=1e-6, atol=1e-6)
+    torch.testing.assert_close(sm.double(), es, rtol=1e-5, atol=0)
+
+
+@pytest.mark.parametrize("split", [1, 3])
+def test_c_tiled_model_within_bf16_p_tolerance(split):
+    data = _small(6, topk=300, length=400)
+    out, mx, sm = O.reference(*data)
+    to, tm, ts = O.c_tiled(*data, tile=64, split=split)
+    assert O.accuracy(to, out)["max_normalized"] < 5e-3
+    assert O.rel_error(tm, mx) < 1e-5
+    assert O.rel_error(ts, sm) < 1e-5
+
+
+def test_uniform_family_closed_form():
+    shape = (1, 1, 128, 8192, 2048)
+    q, kv, qr, kr, ids = review_inputs(shape, 20261103, "uniform")
+    out, mx, sm = O.reference(q, kv, qr, kr, ids)
+    assert torch.all(mx == 0)
+    assert torch.all(sm == 2048)
+    mean = kv[0, ids[0, 0, 0].long(), 0].float().mean(0)
+    torch.testing.assert_close(out[0, 0], mean[None].expand(128, -1), rtol=1e-5, atol=1e-6)
+
+
+def test_index_invariants():
+    q, kv, qr, kr, ids = _small(7, invalid=0.0, dup=0.0)
+    base = O.reference(q, kv, qr, kr, ids)
+    # permutation of slots
+    perm = torch.randperm(ids.shape[-1], generator=torch.Generator().manual_seed(0))
+    for a, b in zip(base, O.reference(q, kv, qr, kr, ids[..., perm].contiguous())):
+        torch.testing.assert_close(a, b, rtol=1e-5, atol=1e-6)
+    # a -1 slot is the same as removing it; >= L is the same as -1
+    cut = ids.clone()
+    cut[..., 5:9] = -1
+    hi = ids.clone()
+    hi[..., 5:9] = kv.shape[1]
+    keep = torch.cat([ids[..., :5], ids[..., 9:]], dim=-1).contiguous()
+    ref = O.reference(q, kv, qr, kr, keep)
+    for a, b, c in zip(ref, O.reference(q, kv, qr, kr, cut), O.reference(q, kv, qr, kr, hi)):
+        torch.testing.assert_close(a, b, rtol=1e-5, atol=1e-6)
+        torch.testing.assert_close(a, c, rtol=1e-5, atol=1e-6)
+    # every slot twice: same output and max, sum doubles
+    twice = torch.cat([ids, ids], dim=-1).contiguous()
+    o2, m2, s2 = O.reference(q, kv, qr, kr, twice)
+    torch.testing.assert_close(o2, base[0], rtol=1e-5, atol=1e-6)
+    torch.testing.assert_close(m2, base[1], rtol=0, atol=0)
+    torch.testing.assert_close(s2, 2 * base[2], rtol=1e-6, atol=0)
