@@ -1,0 +1,254 @@
+"""Benchmark of the MI355X sparse-MLA forward (one JSON line on stdout).
+
+python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c2_decode_b8]
+
+A step is one forward call (main kernel + FP32 split merge) over one batch of
+synthetic inputs already resident in HBM.  The default workload is C2, the
+headline decode case (B=8, SQ=1, H=128, L=32768, TOPK=2048).  Steps cycle
+through ``--rotate`` independent input sets so that the gathered rows come
+from HBM rather than from the 256 MB MALL of a previous identical call; the
+warm (single input set) span is reported beside it.
+
+Timing: HIP events recorded on the launch stream around every call and
+between the main kernel and the merge give the device span per call (the
+``value``), the main-kernel duration (for the roofline) and the merge
+duration; ``ms_per_step`` is the host wall clock of the K timed steps between
+two device synchronisations.
+
+cpu_baseline: the CPU oracle (oracle/dsa_oracle.py, a restatement of the
+reference's FP32 PyTorch gather+softmax path) timed on this host on a bounded
+sample of the same workload.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+import torch
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+import dsa_amd  # noqa: E402
+from dsa_amd import Tuning, _lib  # noqa: E402
+from dsa_amd.workloads import BASELINE_CONFIGS, baseline_inputs  # noqa: E402
+
+METRIC = json.loads((ROOT / "BASELINE.json").read_text())["metric"]
+HBM_PEAK_GBS = 8000.0
+MFMA_PEAK_TFLOPS = 2500.0  # dense bf16
+# Published device span of the reference on Ascend950PR for the same shape
+# (PERFORMANCE_FINAL.md:75 of the reference, decode_b8 task span).
+PUBLISHED_SPAN_US = {"c2_decode_b8": 74.875}
+# Which roofline binds each configuration.
+BOUND = {"c1_decode_b1": "hbm", "c2_decode_b8": "hbm", "c3_decode_h16_mtp": "hbm",
+         "c4_prefill_h16": "mfma", "c5_prefill_h128": "mfma"}
+DEFAULT_ROTATE = {"c1_decode_b1": 16, "c2_decode_b8": 4, "c3_decode_h16_mtp": 1,
+                  "c4_prefill_h16": 1, "c5_prefill_h128": 1}
+
+
+def algorithmic_units(shape):
+    """Gathered bytes and FLOPs of one call: every slot counted once
+    (B*SQ*TOPK rows of 576 bf16) and 2*B*SQ*H*TOPK*(576+512) MFMA FLOPs."""
+    b, sq, h, _, k = shape
+    return b * sq * k * 576 * 2, 2 * b * sq * h * k * (576 + 512)
+
+
+class Call:
+    """One preallocated forward call through the C ABI."""
+
+    def __init__(self, data, config: Tuning):
+        self.data = data
+        q = data[0]
+        self.shape = tuple(q.shape[:3]) + (data[1].shape[1], data[4].shape[-1])
+        b, sq, h, _, _ = self.shape
+        self.config = config
+        self.plan = config.to_c()
+        dev = q.device
+        self.out = torch.empty_like(q)
+        self.mx = torch.empty((b, 1, sq, h), device=dev, dtype=torch.float32)
+        self.sm = torch.empty_like(self.mx)
+        if config.split > 1:
+            self.po = torch.empty((b, sq, config.split, h, 512), device=dev, dtype=torch.float32)
+            self.pm = torch.empty((b, sq, config.split, h), device=dev, dtype=torch.float32)
+            self.pl = torch.empty_like(self.pm)
+        else:
+            self.po = self.pm = self.pl = None
+        p = lambda t: None if t is None else ctypes.c_void_p(t.data_ptr())  # noqa: E731
+        self.args = [p(t) for t in data] + [p(self.out), p(self.mx), p(self.sm), p(self.po), p(self.pm), p(self.pl)]
+        self.lib = _lib.load()
+
+    def main(self, stream):
+        b, sq, h, length, k = self.shape
+        rc = self.lib.dsa_fwd_main(*self.args, b, sq, h, length, k, ctypes.byref(self.plan), stream)
+        if rc:
+            _lib.check(rc, "dsa_fwd_main")
+
+    def merge(self, stream):
+        if self.po is None:
+            return
+        b, sq, h, _, _ = self.shape
+        rc = self.lib.dsa_merge(self.args[8], self.args[9], self.args[10], self.args[5], self.args[6],
+                                self.args[7], b * sq, h, self.config.split, stream)
+        if rc:
+            _lib.check(rc, "dsa_merge")
+
+
+def time_calls(calls, steps, warmup):
+    stream_obj = torch.cuda.current_stream()
+    stream = ctypes.c_void_p(stream_obj.cuda_stream)
+    for i in range(warmup):
+        c = calls[i % len(calls)]
+        c.main(stream)
+        c.merge(stream)
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        c = calls[i % len(calls)]
+        ev[i][0].record(stream_obj)
+        c.main(stream)
+        ev[i][1].record(stream_obj)
+        c.merge(stream)
+        ev[i][2].record(stream_obj)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    main_ms = [e[0].elapsed_time(e[1]) for e in ev]
+    merge_ms = [e[1].elapsed_time(e[2]) for e in ev]
+    span_ms = [e[0].elapsed_time(e[2]) for e in ev]
+    return wall, main_ms, merge_ms, span_ms
+
+
+def cpu_baseline(name, data, budget_s=10.0):
+    """Time the CPU oracle on a bounded sample; scale to µs per full call."""
+    from oracle import dsa_oracle as oracle
+
+    q, kv, qr, kr, ids = (t.cpu() for t in data)
+    batch, queries = q.shape[:2]
+    tokens = [(b, s) for b in range(batch) for s in range(queries)]
+    # sample: whole call when small, else an evenly spaced token subset
+    probe_t = time.perf_counter()
+    oracle.reference(q, kv, qr, kr, ids, tokens=tokens[:1])
+    per_token = max(time.perf_counter() - probe_t, 1e-4)
+    n = len(tokens)
+    if per_token * n > budget_s / 3:
+        n = max(1, int(budget_s / 3 / per_token))
+    sample = tokens[:: max(1, len(tokens) // n)][:n]
+    times = []
+    t_end = time.perf_counter() + budget_s
+    oracle.reference(q, kv, qr, kr, ids, tokens=sample)  # warm-up
+    while time.perf_counter() < t_end or len(times) < 3:
+        t0 = time.perf_counter()
+        oracle.reference(q, kv, qr, kr, ids, tokens=sample)
+        times.append(time.perf_counter() - t0)
+        if len(times) >= 50:
+            break
+    per_call_us = statistics.median(times) * 1e6 * len(tokens) / len(sample)
+    return {"value": round(per_call_us, 1), "unit": "µs/call", "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": (f"FP32 torch gather+softmax oracle on {len(sample)} of {len(tokens)} tokens of one "
+                       f"{name} call, median of {len(times)} runs, scaled to a full call")}
+
+
+def traffic_from_profiles(name):
+    """HBM bytes per main-kernel launch measured by rocprofv3 --pmc, if a
+    summary for this workload is committed under profiles/."""
+    path = ROOT / "profiles" / f"sparse_mla_fwd_{name}_hbm_traffic.json"
+    if not path.exists():
+        return None
+    return json.loads(path.read_text()).get("hbm_bytes_per_launch")
+
+
+def run(name, args):
+    shape = BASELINE_CONFIGS[name]
+    rotate = args.rotate if args.rotate else DEFAULT_ROTATE[name]
+    config = dsa_amd.select(shape)
+    if args.split or args.bm:
+        bm = args.bm or config.bm
+        config = Tuning(bm, 64, args.split or config.split, kv_waves=4 // (bm // 16))
+    print(f"[bench] {name} shape={shape} plan={config} rotate={rotate}", file=sys.stderr, flush=True)
+    sets = [baseline_inputs(name, seed=args.seed + i, device="cuda", cpu_recipe=False) for i in range(rotate)]
+    calls = [Call(d, config) for d in sets]
+    wall, main_ms, merge_ms, span_ms = time_calls(calls, args.steps, args.warmup)
+    warm = time_calls(calls[:1], args.steps, args.warmup)
+    gbytes, flops = algorithmic_units(shape)
+    main_us = statistics.mean(main_ms) * 1e3
+    span_us = statistics.mean(span_ms) * 1e3
+    bound = BOUND[name]
+    if bound == "hbm":
+        achieved, peak, unit = gbytes / (main_us * 1e-6) / 1e9, HBM_PEAK_GBS, "GB/s"
+    else:
+        achieved, peak, unit = flops / (main_us * 1e-6) / 1e12, MFMA_PEAK_TFLOPS, "TFLOP/s"
+    line = {
+        "metric": METRIC,
+        "value": round(span_us, 3),
+        "unit": "µs/call",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall * 1e3 / args.steps, 5),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": (round(span_us / PUBLISHED_SPAN_US[name], 4) if name in PUBLISHED_SPAN_US else None),
+        "dtype": "bf16",
+        "data": (f"synthetic: seeded N(0,1) bf16 q/kv/rope, per-workload index recipe, "
+                 f"{rotate} rotating input set(s) resident in HBM"),
+        "config": {"workload": name, "B": shape[0], "SQ": shape[1], "H": shape[2], "L": shape[3],
+                   "TOPK": shape[4], "plan": vars(config) if hasattr(config, "__dict__") else str(config),
+                   "rotating_input_sets": rotate},
+        "roofline": {"bound": bound, "achieved": round(achieved, 2), "peak": peak, "unit": unit,
+                     "frac": round(achieved / peak, 4), "traffic": traffic_from_profiles(name),
+                     "kernel": f"sparse_mla_fwd (main), {gbytes} gathered B and {flops} FLOP per launch"},
+        "breakdown": {
+            "span_us_mean": round(span_us, 3),
+            "span_us_median": round(statistics.median(span_ms) * 1e3, 3),
+            "main_us_mean": round(main_us, 3),
+            "merge_us_mean": round(statistics.mean(merge_ms) * 1e3, 3),
+            "warm_span_us_mean": round(statistics.mean(warm[3]) * 1e3, 3),
+            "warm_main_us_mean": round(statistics.mean(warm[1]) * 1e3, 3),
+            "gathered_TBps_main": round(gbytes / (main_us * 1e-6) / 1e12, 3),
+            "mfma_TFLOPs_main": round(flops / (main_us * 1e-6) / 1e12, 2),
+            "gathered_TBps_span": round(gbytes / (span_us * 1e-6) / 1e12, 3),
+            "mfma_TFLOPs_span": round(flops / (span_us * 1e-6) / 1e12, 2),
+        },
+    }
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline(name, sets[0], args.cpu_budget)
+    return line
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--config", default="c2_decode_b8", choices=sorted(BASELINE_CONFIGS))
+    ap.add_argument("--all", action="store_true", help="one line per configuration C2..C5")
+    ap.add_argument("--rotate", type=int, default=0, help="input sets to cycle (default per workload)")
+    ap.add_argument("--split", type=int, default=0, help="override the plan's KV split")
+    ap.add_argument("--bm", type=int, default=0, help="override heads per workgroup (16/32/64)")
+    ap.add_argument("--seed", type=int, default=20261102)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU oracle timing")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (each GPU box has one "
+              "MI355X); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        sys.exit(2)
+    torch.cuda.init()
+    names = ["c2_decode_b8", "c3_decode_h16_mtp", "c4_prefill_h16", "c5_prefill_h128"] if args.all else [args.config]
+    for name in names:
+        line = run(name, args)
+        print(json.dumps(line, ensure_ascii=False), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -38,6 +38,8 @@ SIGNATURES = {
                                  ctypes.POINTER(_i64), ctypes.POINTER(_i64)]),
     "dsa_fwd": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                        _i32, _i32, _i32, _i32, _i32, ctypes.POINTER(DsaPlan), _vp]),
+    "dsa_fwd_main": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                            _i32, _i32, _i32, _i32, _i32, ctypes.POINTER(DsaPlan), _vp]),
     "dsa_merge": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _vp]),
 }
 

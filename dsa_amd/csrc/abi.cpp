@@ -119,14 +119,21 @@ int dsa_merge(const float* part_o, const float* part_m, const float* part_l, uin
     return 0;
 }
 
-int dsa_fwd(const uint16_t* q, const uint16_t* kv, const uint16_t* q_rope, const uint16_t* k_rope,
-            const int32_t* idx, uint16_t* out, float* out_max, float* out_sum, float* part_o, float* part_m,
-            float* part_l, int B, int SQ, int H, int L, int TOPK, const dsa_plan* plan, hipStream_t stream) {
-    if (!q || !kv || !q_rope || !k_rope || !idx || !out || !out_max || !out_sum)
-        return fail(-1, "NULL input/output pointer");
+}  // extern "C"
+
+namespace {
+
+// Shared by dsa_fwd and dsa_fwd_main: validate, resolve the plan, launch the
+// main kernel and, when `with_merge` and split > 1, the merge.
+int fwd_impl(const uint16_t* q, const uint16_t* kv, const uint16_t* q_rope, const uint16_t* k_rope,
+             const int32_t* idx, uint16_t* out, float* out_max, float* out_sum, float* part_o, float* part_m,
+             float* part_l, int B, int SQ, int H, int L, int TOPK, const dsa_plan* plan, hipStream_t stream,
+             bool with_merge) {
+    if (!q || !kv || !q_rope || !k_rope || !idx) return fail(-1, "NULL input pointer");
     if (int rc = check_shape(B, SQ, H, L, TOPK)) return rc;
     dsa_plan local{};
     if (!plan) {
+        if (!with_merge) return fail(-1, "dsa_fwd_main needs an explicit plan");
         int dev = 0, cus = 0;
         int err = (int)hipGetDevice(&dev);
         if (!err) err = (int)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
@@ -136,12 +143,17 @@ int dsa_fwd(const uint16_t* q, const uint16_t* kv, const uint16_t* q_rope, const
     } else if (int rc = dsa_plan_check(plan, B, SQ, H, L, TOPK)) {
         return rc;
     }
-    if (plan->split > 1 && (!part_o || !part_m || !part_l))
+    const bool split = plan->split > 1;
+    if ((!split || with_merge) && (!out || !out_max || !out_sum)) return fail(-1, "NULL output pointer");
+    if (split && (!part_o || !part_m || !part_l))
         return fail(-1, "split=%d needs part_o, part_m and part_l", plan->split);
     // 16-byte vector accesses need 16-byte aligned rows.
-    if (((uintptr_t)q | (uintptr_t)kv | (uintptr_t)q_rope | (uintptr_t)k_rope | (uintptr_t)out) & 15)
-        return fail(-1, "q, kv, q_rope, k_rope and out must be 16-byte aligned");
-    if (plan->split > 1 && ((uintptr_t)part_o & 15)) return fail(-1, "part_o must be 16-byte aligned");
+    if (((uintptr_t)q | (uintptr_t)kv | (uintptr_t)q_rope | (uintptr_t)k_rope) & 15)
+        return fail(-1, "q, kv, q_rope and k_rope must be 16-byte aligned");
+    if (out && ((uintptr_t)out & 15)) return fail(-1, "out must be 16-byte aligned");
+    if (split && ((uintptr_t)part_o & 15)) return fail(-1, "part_o must be 16-byte aligned");
+    const int64_t rowgroups = (int64_t)B * SQ * plan->split;
+    if (rowgroups * (H / plan->heads_per_group) > 0x7fffffff) return fail(-1, "grid too large");
 
     dsa::FwdParams p{};
     p.q = q;
@@ -163,17 +175,35 @@ int dsa_fwd(const uint16_t* q, const uint16_t* kv, const uint16_t* q_rope, const
     p.nsplit = plan->split;
     p.ntiles = ceil_div(TOPK, plan->tile_rows);
     p.hgroups = H / plan->heads_per_group;
-    p.rowgroups = B * SQ * plan->split;
-    if (dsa::fwd_grid(p) > 0x7fffffff) return fail(-1, "grid too large");
+    p.rowgroups = (int)rowgroups;
 
     int rc = dsa::launch_fwd(p, plan->heads_per_group, plan->kv_waves, plan->tile_rows, plan->stages, stream);
     if (rc) return hip_fail(rc, "main kernel launch");
-    if (plan->split > 1) {
+    if (split && with_merge) {
         rc = dsa::launch_merge(part_o, part_m, part_l, out, out_max, out_sum, B * SQ, H, plan->split, stream);
         if (rc) return hip_fail(rc, "merge launch");
     }
     g_err[0] = 0;
     return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+int dsa_fwd(const uint16_t* q, const uint16_t* kv, const uint16_t* q_rope, const uint16_t* k_rope,
+            const int32_t* idx, uint16_t* out, float* out_max, float* out_sum, float* part_o, float* part_m,
+            float* part_l, int B, int SQ, int H, int L, int TOPK, const dsa_plan* plan, hipStream_t stream) {
+    return fwd_impl(q, kv, q_rope, k_rope, idx, out, out_max, out_sum, part_o, part_m, part_l, B, SQ, H, L,
+                    TOPK, plan, stream, true);
+}
+
+int dsa_fwd_main(const uint16_t* q, const uint16_t* kv, const uint16_t* q_rope, const uint16_t* k_rope,
+                 const int32_t* idx, uint16_t* out, float* out_max, float* out_sum, float* part_o,
+                 float* part_m, float* part_l, int B, int SQ, int H, int L, int TOPK, const dsa_plan* plan,
+                 hipStream_t stream) {
+    return fwd_impl(q, kv, q_rope, k_rope, idx, out, out_max, out_sum, part_o, part_m, part_l, B, SQ, H, L,
+                    TOPK, plan, stream, false);
 }
 
 }  // extern "C"

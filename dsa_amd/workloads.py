@@ -70,10 +70,13 @@ def _subset_rows(n_rows, length, k, gen, device, limit=None):
     return keys.topk(k, dim=1, largest=False).indices.int()
 
 
-def baseline_inputs(name: str, seed: int = REVIEW_SEED, device="cuda"):
+def baseline_inputs(name: str, seed: int = REVIEW_SEED, device="cuda", cpu_recipe: bool = True):
     """Inputs of MI355X benchmark configuration ``name`` on ``device``.
 
-    c1, c2: the reference recipe (family normal), generated on the CPU.
+    c1, c2: the reference recipe (family normal), generated on the CPU; with
+        ``cpu_recipe=False`` the same distribution is drawn on ``device``
+        (N(0,1) bf16, distinct uniform indices per token) -- much faster for
+        the benchmark's rotating input sets.
     c3: N(0,1) bf16; per token ``TOPK`` distinct indices uniform over [0, L).
     c4: query i sits at position 4096 + i; its indices are distinct and
         uniform over [0, 4096 + i] (all valid).
@@ -84,7 +87,7 @@ def baseline_inputs(name: str, seed: int = REVIEW_SEED, device="cuda"):
     """
     shape = BASELINE_CONFIGS[name]
     batch, queries, heads, length, k = shape
-    if name in ("c1_decode_b1", "c2_decode_b8"):
+    if name in ("c1_decode_b1", "c2_decode_b8") and cpu_recipe:
         return tuple(t.to(device) for t in review_inputs(shape, seed, "normal"))
     gen = torch.Generator(device=device).manual_seed(seed)
     q = _normal_bf16((batch, queries, heads, 512), gen, device)
@@ -92,7 +95,7 @@ def baseline_inputs(name: str, seed: int = REVIEW_SEED, device="cuda"):
     qr = _normal_bf16((batch, queries, heads, 64), gen, device)
     kr = _normal_bf16((batch, length, 1, 64), gen, device)
     tokens = batch * queries
-    if name == "c3_decode_h16_mtp":
+    if name in ("c1_decode_b1", "c2_decode_b8", "c3_decode_h16_mtp"):
         ids = torch.cat([_subset_rows(min(32, tokens - i), length, k, gen, device)
                          for i in range(0, tokens, 32)])
     elif name == "c4_prefill_h16":

@@ -111,6 +111,20 @@ int dsa_fwd(const uint16_t* q, const uint16_t* kv, const uint16_t* q_rope,
             const dsa_plan* plan, hipStream_t stream);
 
 /*
+ * The main kernel of dsa_fwd alone (dsa/api.py:115-123): with plan->split == 1
+ * it writes out/out_max/out_sum; with split > 1 it writes only the partials
+ * and the caller completes the call with dsa_merge (for example after
+ * combining partials computed over different KV shards).  plan must be
+ * non-NULL here.
+ */
+int dsa_fwd_main(const uint16_t* q, const uint16_t* kv, const uint16_t* q_rope,
+                 const uint16_t* k_rope, const int32_t* idx,
+                 uint16_t* out, float* out_max, float* out_sum,
+                 float* part_o, float* part_m, float* part_l,
+                 int B, int SQ, int H, int L, int TOPK,
+                 const dsa_plan* plan, hipStream_t stream);
+
+/*
  * FP32 merge of split partials (dsa/merge.py:13-91):
  *   m = max_s m_s;  w_s = exp(m_s - m);  l = sum_s w_s l_s;
  *   out = bf16(sum_s w_s u_s / l);  out_max = m;  out_sum = l.

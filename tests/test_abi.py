@@ -22,7 +22,7 @@ def declared_functions():
 def test_header_declares_the_expected_entry_points():
     assert declared_functions() == sorted(
         ["dsa_version", "dsa_last_error", "dsa_plan_for", "dsa_plan_check", "dsa_partial_elems",
-         "dsa_fwd", "dsa_merge"])
+         "dsa_fwd", "dsa_fwd_main", "dsa_merge"])
 
 
 def test_library_exports_every_declared_symbol():
@@ -61,6 +61,9 @@ def test_fwd_and_merge_validate_before_any_launch():
                      1, 1, 16, 10, 10, None, None)
     assert rc < 0 and b"NULL" in lib.dsa_last_error()
     rc = lib.dsa_merge(null, null, null, null, null, null, 1, 16, 2, None)
+    assert rc < 0
+    rc = lib.dsa_fwd_main(null, null, null, null, null, null, null, null, null, null, null,
+                          1, 1, 16, 10, 10, None, None)
     assert rc < 0
 
 
