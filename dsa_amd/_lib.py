@@ -25,7 +25,8 @@ class DsaPlan(ctypes.Structure):
         ("split", ctypes.c_int32),
         ("kv_waves", ctypes.c_int32),
         ("stages", ctypes.c_int32),
-        ("reserved", ctypes.c_int32 * 3),
+        ("mfma", ctypes.c_int32),
+        ("reserved", ctypes.c_int32 * 2),
     ]
 
 

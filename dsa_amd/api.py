@@ -78,7 +78,8 @@ def plan_call(shape, config=None, cores: int = 256):
         check_tuning(config, shape)
     batch, queries, heads, _, _ = shape
     tokens = batch * queries
-    launches = [Launch(f"sparse_mla_fwd_h{config.bm}_kw{config.kv_waves}_bn{config.bn}_s{config.stages}",
+    variant = "wide" if config.mfma == 32 else "narrow"
+    launches = [Launch(f"sparse_mla_fwd_{variant}_h{config.bm}_kw{config.kv_waves}_bn{config.bn}_s{config.stages}",
                        tokens * config.split * (heads // config.bm), 256, _LDS_BYTES)]
     partials = None
     if config.split > 1:

@@ -4,12 +4,14 @@ Replaces dsa/config.py of the reference (Tuning :10-19, CASE_SHAPES :23-40,
 SELECTED :42-59, select :64-69).  The reference's Tuning fields described an
 Ascend Cube/Vector pipeline; here the plan describes gfx950 workgroups:
 
-* ``bm``       -- query heads per workgroup (16, 32 or 64; divides H);
+* ``bm``       -- query heads per workgroup (divides H);
 * ``bn``       -- gathered rows per LDS ring stage (64);
 * ``split``    -- KV splits per (token, head group); > 1 adds the FP32 merge;
 * ``kv_waves`` -- waves that share a head slice and split each tile's rows
-                  (``bm // 16 * kv_waves == 4``: four waves per workgroup);
-* ``stages``   -- LDS ring depth (2).
+                  (``bm // mfma * kv_waves == 4``: four waves per workgroup);
+* ``stages``   -- LDS ring depth (2);
+* ``mfma``     -- heads per wave: 32 (v_mfma_f32_32x32x16_bf16, bm 64 with
+                  kv_waves 2) or 16 (v_mfma_f32_16x16x32_bf16, bm 64, 32 or 16).
 
 Unlike the reference, shapes outside the table are accepted: the library's
 planner (``dsa_plan_for``) derives a plan for any supported shape.
@@ -31,16 +33,17 @@ class Tuning:
     split: int
     kv_waves: int = 1
     stages: int = 2
+    mfma: int = 32
 
     def to_c(self) -> _lib.DsaPlan:
         p = _lib.DsaPlan()
         p.heads_per_group, p.tile_rows, p.split = self.bm, self.bn, self.split
-        p.kv_waves, p.stages = self.kv_waves, self.stages
+        p.kv_waves, p.stages, p.mfma = self.kv_waves, self.stages, self.mfma
         return p
 
     @staticmethod
     def from_c(p: _lib.DsaPlan) -> "Tuning":
-        return Tuning(p.heads_per_group, p.tile_rows, p.split, p.kv_waves, p.stages)
+        return Tuning(p.heads_per_group, p.tile_rows, p.split, p.kv_waves, p.stages, p.mfma)
 
 
 # (batch, query length, heads, KV length, number of selected indices).
@@ -87,7 +90,8 @@ def check_tuning(config: Tuning, shape) -> None:
     """Validate a caller-supplied plan (reference: dsa/api.py:41-60)."""
     if not isinstance(config, Tuning):
         raise TypeError("config must be a dsa_amd.Tuning")
-    if any(type(v) is not int for v in (config.bm, config.bn, config.split, config.kv_waves, config.stages)):
+    if any(type(v) is not int
+           for v in (config.bm, config.bn, config.split, config.kv_waves, config.stages, config.mfma)):
         raise ValueError("Tuning fields must be int")
     b, sq, h, length, topk = shape
     plan = config.to_c()
@@ -96,29 +100,30 @@ def check_tuning(config: Tuning, shape) -> None:
 
 # Per-shape plans for MI355X (256 CUs), re-derived from the reference's table
 # (dsa/config.py:42-59) for gfx950: four waves per workgroup, one 152 KiB
-# workgroup per CU, KV split until the grid covers the CUs.
+# workgroup per CU, 32-head waves wherever H is a multiple of 64, KV split
+# until the grid covers the CUs.
 SELECTED = {
-    "decode_b1": Tuning(64, 64, 32),
-    "decode_b8": Tuning(64, 64, 16),
-    "decode_b32": Tuning(64, 64, 4),
-    "decode_tp8": Tuning(16, 64, 32, kv_waves=4),
-    "prefill_q16": Tuning(64, 64, 8),
-    "prefill_q64": Tuning(64, 64, 2),
-    "prefill_tp8": Tuning(16, 64, 2, kv_waves=4),
-    "prefill_k512": Tuning(64, 64, 2),
-    "decode_b4_h128": Tuning(64, 64, 32),
-    "prefill_b4_h128": Tuning(64, 64, 1),
-    "decode_b4_h64": Tuning(64, 64, 32),
-    "prefill_b4_h64": Tuning(64, 64, 1),
-    "decode_b4_h32": Tuning(32, 64, 32, kv_waves=2),
-    "prefill_b4_h32": Tuning(32, 64, 1, kv_waves=2),
-    "decode_b4_h16": Tuning(16, 64, 32, kv_waves=4),
-    "prefill_b4_h16": Tuning(16, 64, 1, kv_waves=4),
-    "c1_decode_b1": Tuning(64, 64, 32),
-    "c2_decode_b8": Tuning(64, 64, 16),
-    "c3_decode_h16_mtp": Tuning(16, 64, 2, kv_waves=4),
-    "c4_prefill_h16": Tuning(16, 64, 1, kv_waves=4),
-    "c5_prefill_h128": Tuning(64, 64, 1),
+    "decode_b1": Tuning(64, 64, 32, kv_waves=2),
+    "decode_b8": Tuning(64, 64, 16, kv_waves=2),
+    "decode_b32": Tuning(64, 64, 4, kv_waves=2),
+    "decode_tp8": Tuning(16, 64, 32, kv_waves=4, mfma=16),
+    "prefill_q16": Tuning(64, 64, 8, kv_waves=2),
+    "prefill_q64": Tuning(64, 64, 2, kv_waves=2),
+    "prefill_tp8": Tuning(16, 64, 2, kv_waves=4, mfma=16),
+    "prefill_k512": Tuning(64, 64, 2, kv_waves=2),
+    "decode_b4_h128": Tuning(64, 64, 32, kv_waves=2),
+    "prefill_b4_h128": Tuning(64, 64, 1, kv_waves=2),
+    "decode_b4_h64": Tuning(64, 64, 32, kv_waves=2),
+    "prefill_b4_h64": Tuning(64, 64, 1, kv_waves=2),
+    "decode_b4_h32": Tuning(32, 64, 32, kv_waves=2, mfma=16),
+    "prefill_b4_h32": Tuning(32, 64, 1, kv_waves=2, mfma=16),
+    "decode_b4_h16": Tuning(16, 64, 32, kv_waves=4, mfma=16),
+    "prefill_b4_h16": Tuning(16, 64, 1, kv_waves=4, mfma=16),
+    "c1_decode_b1": Tuning(64, 64, 32, kv_waves=2),
+    "c2_decode_b8": Tuning(64, 64, 16, kv_waves=2),
+    "c3_decode_h16_mtp": Tuning(16, 64, 2, kv_waves=4, mfma=16),
+    "c4_prefill_h16": Tuning(16, 64, 1, kv_waves=4, mfma=16),
+    "c5_prefill_h128": Tuning(64, 64, 1, kv_waves=2),
 }
 _BY_SHAPE = {}
 for _name, _shape in CASE_SHAPES.items():

@@ -54,16 +54,17 @@ const char* dsa_last_error(void) { return g_err; }
 int dsa_plan_check(const dsa_plan* plan, int B, int SQ, int H, int L, int TOPK) {
     if (!plan) return fail(-1, "plan is NULL");
     if (int rc = check_shape(B, SQ, H, L, TOPK)) return rc;
-    const int hpg = plan->heads_per_group, bn = plan->tile_rows, split = plan->split;
-    if (hpg != 16 && hpg != 32 && hpg != 64)
-        return fail(-1, "heads_per_group must be 16, 32 or 64 (got %d)", hpg);
+    const int hpg = plan->heads_per_group, bn = plan->tile_rows, split = plan->split, mfma = plan->mfma;
+    if (mfma != 16 && mfma != 32) return fail(-1, "mfma must be 16 or 32 (got %d)", mfma);
+    if (hpg <= 0 || hpg % mfma)
+        return fail(-1, "heads_per_group must be a positive multiple of mfma=%d (got %d)", mfma, hpg);
     if (H % hpg) return fail(-1, "heads_per_group %d must divide H=%d", hpg, H);
     if (bn != kTileRows) return fail(-1, "tile_rows must be %d (got %d)", kTileRows, bn);
     if (plan->stages != kStages) return fail(-1, "stages must be %d (got %d)", kStages, plan->stages);
-    if (plan->kv_waves * (hpg / 16) != 4)
-        return fail(-1, "kv_waves * heads_per_group / 16 must be 4 (got kv_waves=%d)", plan->kv_waves);
-    if (!dsa::fwd_variant_exists(hpg, plan->kv_waves, bn, plan->stages))
-        return fail(-1, "no kernel variant for this plan");
+    if (plan->kv_waves * (hpg / mfma) != 4)
+        return fail(-1, "kv_waves * heads_per_group / mfma must be 4 (got kv_waves=%d)", plan->kv_waves);
+    if (!dsa::fwd_variant_exists(hpg, plan->kv_waves, bn, plan->stages, mfma))
+        return fail(-1, "no kernel variant for heads_per_group=%d kv_waves=%d mfma=%d", hpg, plan->kv_waves, mfma);
     const int ntiles = ceil_div(TOPK, bn);
     if (split < 1 || split > ntiles)
         return fail(-1, "split must be in [1, %d] for TOPK=%d (got %d)", ntiles, TOPK, split);
@@ -78,15 +79,23 @@ int dsa_plan_for(int B, int SQ, int H, int L, int TOPK, int num_cus, dsa_plan* o
     if (int rc = check_shape(B, SQ, H, L, TOPK)) return rc;
     if (num_cus <= 0) return fail(-1, "num_cus must be positive (got %d)", num_cus);
     dsa_plan p{};
-    // Four waves per workgroup: 64 heads x 1 row stream, 32 x 2 or 16 x 4.
-    p.heads_per_group = (H % 64 == 0) ? 64 : (H % 32 == 0) ? 32 : 16;
-    p.kv_waves = 4 / (p.heads_per_group / 16);
+    // Four waves per workgroup.  Head counts that are multiples of 64 use the
+    // 32x32x16 MFMA variant (32 heads per wave, 64 heads x 2 row streams);
+    // other head counts use the 16x16x32 variant: 32 x 2 or 16 x 4.
+    const int64_t tokens = (int64_t)B * SQ;
+    if (H % 64 == 0) {
+        p.heads_per_group = 64, p.kv_waves = 2, p.mfma = 32;
+    } else if (H % 32 == 0) {
+        p.heads_per_group = 32, p.kv_waves = 2, p.mfma = 16;
+    } else {
+        p.heads_per_group = 16, p.kv_waves = 4, p.mfma = 16;
+    }
     p.tile_rows = kTileRows;
     p.stages = kStages;
     // One 152 KiB workgroup fits a CU; split the KV range until the grid covers
     // every CU once, but never below one tile per split.
     const int ntiles = ceil_div(TOPK, kTileRows);
-    const int64_t base = (int64_t)B * SQ * (H / p.heads_per_group);
+    const int64_t base = tokens * (H / p.heads_per_group);
     int split = 1;
     if (base < num_cus) split = (int)((num_cus + base - 1) / base);
     if (split > ntiles) split = ntiles;
@@ -177,7 +186,8 @@ int fwd_impl(const uint16_t* q, const uint16_t* kv, const uint16_t* q_rope, cons
     p.hgroups = H / plan->heads_per_group;
     p.rowgroups = (int)rowgroups;
 
-    int rc = dsa::launch_fwd(p, plan->heads_per_group, plan->kv_waves, plan->tile_rows, plan->stages, stream);
+    int rc = dsa::launch_fwd(p, plan->heads_per_group, plan->kv_waves, plan->tile_rows, plan->stages, plan->mfma,
+                             stream);
     if (rc) return hip_fail(rc, "main kernel launch");
     if (split && with_merge) {
         rc = dsa::launch_merge(part_o, part_m, part_l, out, out_max, out_sum, B * SQ, H, plan->split, stream);

@@ -29,15 +29,15 @@ struct FwdParams {
 };
 
 // Kernel variants compiled into the library, keyed by
-// (heads_per_group, kv_waves, tile_rows, stages).
-bool fwd_variant_exists(int heads_per_group, int kv_waves, int tile_rows, int stages);
+// (heads_per_group, kv_waves, tile_rows, stages, mfma).
+bool fwd_variant_exists(int heads_per_group, int kv_waves, int tile_rows, int stages, int mfma);
 
 // Grid size (workgroups) of the main kernel for these params/plan.
 int64_t fwd_grid(const FwdParams& p);
 
 // Enqueue the main kernel; returns a hipError_t.
 int launch_fwd(const FwdParams& p, int heads_per_group, int kv_waves, int tile_rows,
-               int stages, hipStream_t stream);
+               int stages, int mfma, hipStream_t stream);
 
 // Enqueue the split merge; returns a hipError_t.
 int launch_merge(const float* part_o, const float* part_m, const float* part_l,

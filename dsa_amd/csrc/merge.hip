@@ -3,7 +3,8 @@
 //   m = max_s m_s;  w_s = exp(m_s - m);  l = sum_s w_s * l_s;
 //   out = bf16(sum_s w_s * u_s / l);  out_max = m;  out_sum = l.
 // One workgroup merges two heads of one token; each thread owns 4 of the 512
-// columns and streams the split partials with 16-byte loads.
+// columns and streams the split partials with 16-byte loads, kBatch splits in
+// flight at a time.
 #include <hip/hip_runtime.h>
 #include <float.h>
 #include <stdint.h>
@@ -17,6 +18,8 @@ typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;
 typedef __attribute__((__vector_size__(4 * sizeof(__bf16)))) __bf16 bf16x4;
 
 constexpr float kLog2e = 1.4426950408889634f;
+
+constexpr int kBatch = 8;  // split partials loaded per batch (kept in flight together)
 
 __global__ __launch_bounds__(256) void merge_kernel(const float* __restrict__ part_o,
                                                     const float* __restrict__ part_m,
@@ -32,15 +35,32 @@ __global__ __launch_bounds__(256) void merge_kernel(const float* __restrict__ pa
     const int64_t base = (int64_t)token * nsplit * H + h;  // + s * H
 
     float m = -FLT_MAX;
-    for (int s = 0; s < nsplit; ++s) m = fmaxf(m, part_m[base + (int64_t)s * H]);
+    for (int s0 = 0; s0 < nsplit; s0 += kBatch) {
+        float ms[kBatch];
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j) ms[j] = s0 + j < nsplit ? part_m[base + (int64_t)(s0 + j) * H] : -FLT_MAX;
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j) m = fmaxf(m, ms[j]);
+    }
     float l = 0.f;
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    for (int s = 0; s < nsplit; ++s) {
-        const int64_t row = base + (int64_t)s * H;
-        const float w = __builtin_amdgcn_exp2f((part_m[row] - m) * kLog2e);
-        l += w * part_l[row];
-        const f32x4 u = *reinterpret_cast<const f32x4*>(part_o + row * 512 + col);
-        acc += w * u;
+    for (int s0 = 0; s0 < nsplit; s0 += kBatch) {
+        f32x4 u[kBatch];
+        float ms[kBatch], ls[kBatch];
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j) {
+            const bool live = s0 + j < nsplit;
+            const int64_t row = base + (int64_t)(live ? s0 + j : 0) * H;
+            ms[j] = live ? part_m[row] : -FLT_MAX;
+            ls[j] = live ? part_l[row] : 0.f;
+            u[j] = live ? *reinterpret_cast<const f32x4*>(part_o + row * 512 + col) : f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j) {
+            const float w = __builtin_amdgcn_exp2f((ms[j] - m) * kLog2e);
+            l += w * ls[j];
+            acc += w * u[j];
+        }
     }
     bf16x4 o;
     o[0] = (__bf16)(acc[0] / l);

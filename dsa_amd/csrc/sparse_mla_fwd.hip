@@ -1,27 +1,33 @@
 // Sparse-MLA attention forward for gfx950 (MI355X).
 //
-// One workgroup owns (token, KV split, head group).  It gathers the selected
-// 576-wide rows (kv[:512] ++ k_rope[:64]) straight from HBM into an LDS ring
-// with global_load_lds_dwordx4 (no VGPR staging), and every wave computes, for
-// its 16 heads,
+// One workgroup (4 waves) owns (token, KV split, head group).  It gathers the
+// selected 576-wide rows (kv[:512] ++ k_rope[:64]) straight from HBM into a
+// two-stage LDS ring with global_load_lds_dwordx4 (no VGPR staging); every
+// wave then computes, for its slice of heads and rows,
 //
-//   S^T[row, head] = K[row, :576] . Q[head, :576]      (v_mfma_f32_16x16x32_bf16,
-//                                                       A = K from LDS, B = Q in VGPRs)
+//   S^T[row, head] = K[row, :576] . Q[head, :576]       A = K from LDS, B = Q in VGPRs
 //   online softmax over rows in registers (log2 units, FP32 state)
-//   O^T[col, head] += V^T[col, row] . P^T[row, head]   (A = V read with
-//                                                       ds_read_b64_tr_b16, B = P in VGPRs)
+//   O^T[col, head] += V^T[col, row] . P^T[row, head]    A = V read with ds_read_b64_tr_b16,
+//                                                        B = P in VGPRs
 //
-// S^T puts the head on lane & 15, which is exactly the lane layout the PV
-// B operand needs, so P never leaves registers.  All heads of the group share
-// one gathered tile.
+// S^T puts the head on the lane index, which is exactly the lane layout the
+// PV B operand needs, so P never leaves registers; all heads of the group
+// share one gathered tile.  Two variants:
+//
+//   wide   -- v_mfma_f32_32x32x16_bf16, 32 heads per wave (Q: 144 VGPRs,
+//             O: 256 accumulators), 2 head-waves x 2 row-waves = 64 heads per
+//             workgroup.  Twice the operand reuse per LDS byte of the narrow
+//             variant and the full-rate MFMA on gfx950.
+//   narrow -- v_mfma_f32_16x16x32_bf16, 16 heads per wave; for head counts
+//             that are not a multiple of 64 (H = 16, 32, 48, ...).
 //
 // Math follows the reference workspace kernel (dsa/workspace.py:242-390):
 // running max initialised to -FLT_MAX (:68), scores scaled and masked by the
-// raw index (:252-257), alpha = exp(m_old - m_new), FP32 sum of the FP32
-// exponentials, P rounded to bf16 (RNE) before PV (:270-272), FP32 accumulation,
-// and for split > 1 the unnormalised FP32 numerator plus (max, sum) partials
-// (:379-385).  Scores are carried in log2 units (x * log2(e)/24) so that every
-// exponential is one v_exp_f32; max/sum leave the kernel in natural units.
+// raw index (:252-257), FP32 sum of the FP32 exponentials, P rounded to bf16
+// (RNE) before PV (:270-272), FP32 accumulation, and for split > 1 the
+// unnormalised FP32 numerator plus (max, sum) partials (:379-385).  Scores are
+// carried in log2 units (x * log2(e)/24) so that every exponential is one
+// v_exp_f32; max/sum leave the kernel in natural units.
 #include <hip/hip_runtime.h>
 #include <float.h>
 #include <stdint.h>
@@ -36,15 +42,40 @@ typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
 typedef __attribute__((__vector_size__(4 * sizeof(__bf16)))) __bf16 bf16x4;
 typedef __attribute__((__vector_size__(4 * sizeof(short)))) short i16x4;
 typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;
+typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16;
 typedef __attribute__((__vector_size__(4 * sizeof(int)))) int i32x4;
 
 // log2(e) / 24: multiplying the raw QK dot product by this gives the score in
 // log2 units, so exp(score - max) == exp2(x - x_max).
 constexpr float kScoreLog2 = (float)(1.4426950408889634 / 24.0);
 constexpr float kLn2 = 0.69314718055994531f;
+// Narrow variant: P is formed against a reference max m_ref that only moves
+// when the true running max exceeds it by more than this (log2 units); then
+// O and l are rescaled.  P <= 2^8, so bf16 P keeps its relative precision.
+constexpr float kRescaleLog2 = 8.0f;
+// Wide variant: m_ref is fixed at the first tile with a valid row and P <=
+// 2^kRestartLog2; a head whose running max exceeds m_ref by more than that
+// makes the workgroup recompute its range once with m_ref = the exact max.
+// This keeps the 256 O accumulators out of VALU work inside the loop.
+constexpr float kRestartLog2 = 64.0f;
+
+// ------------------------------------------------------------ ring layout
+// 4 waves, 64-row tiles, 2 stages: [stage][64 rows][1024 B kv] then
+// [stage][64 rows][128 B rope], then the slot indices of the workgroup.
+constexpr int kWaves = 4;
+constexpr int kThreads = 64 * kWaves;
+constexpr int kBN = 64;
+constexpr int kKvBytes = kBN * 1024;
+constexpr int kRopeBytes = kBN * 128;
+constexpr int kStageBytes = kKvBytes + kRopeBytes;
+constexpr int kIdxOff = 2 * kStageBytes;
+constexpr int kGenOff = kIdxOff + DSA_IDX_CAP * 4;  // second-pass vote (wide variant)
+constexpr int kLdsBytes = kGenOff + 16;
+constexpr int kKvPerWave = kBN / kWaves;          // kv row gathers per wave per tile
+constexpr int kRopePerWave = kBN / 8 / kWaves;    // rope gathers (8 rows each)
+static_assert(kLdsBytes <= 160 * 1024, "LDS budget");
 
 // ---------------------------------------------------------------- LDS access
-// LDS is addressed through 32-bit byte addresses in address space 3.
 template <typename T>
 __device__ __forceinline__ T lds_load(uint32_t addr) {
     return *reinterpret_cast<__attribute__((address_space(3))) T*>(addr);
@@ -67,99 +98,49 @@ __device__ __forceinline__ void lds_barrier() {
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
-// s_waitcnt vmcnt(N), other counters untouched (gfx9 encoding).
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-    static_assert(N >= 0 && N < 64, "vmcnt range");
-    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+// s_waitcnt vmcnt(0), other counters untouched (gfx9 encoding).
+__device__ __forceinline__ void wait_vmcnt0() {
+    __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
 }
 
 // Gather one 16-byte chunk per lane from global memory into LDS at
-// m0 + 16 * lane.  Issued as inline asm so the compiler does not serialise
-// later LDS reads behind it; completion is tracked with wait_vmcnt().
+// m0 + 16 * lane (the LDS base is wave-uniform by construction).  Issued as
+// inline asm so the compiler does not serialise later LDS reads behind it;
+// completion is tracked with wait_vmcnt0().
 __device__ __forceinline__ void gather16(uint32_t lds_wave_base, const void* gaddr) {
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
     asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off"
                  :
-                 : "s"(lds_wave_base), "v"(gaddr)
+                 : "s"(__builtin_amdgcn_readfirstlane(lds_wave_base)), "v"(gaddr)
                  : "memory", "m0");
 #pragma clang diagnostic pop
 }
 
 // 16-byte chunk swizzles.  A kv row occupies 1024 contiguous LDS bytes (64
-// chunks); logical chunk c of tile row r lives at physical chunk c ^ sw_kv(r).
-// A rope row occupies 128 bytes (8 chunks): physical = c ^ sw_rope(r).  The
-// swizzles make both the QK reads (16 rows x 16 B per quarter-wave) and the
-// transposed PV reads (8 rows x 32 B per half-wave) bank-conflict free.
-__device__ __forceinline__ int sw_kv(int r) { return ((r & 7) << 1) | ((r >> 3) & 1); }
+// chunks); logical chunk c of tile row r lives at physical chunk c ^ sw_kv(r)
+// (only the low 4 bits move).  sw_kv is a permutation of 0..15 whose values
+// differ in bits [3:2] within every group of 4 consecutive rows and in bits
+// [3:1] within every group of 8, which makes the QK reads (16 rows x 16 B per
+// quarter-wave) and the transposed PV reads of both variants bank-conflict
+// free.  A rope row occupies 128 bytes (8 chunks): physical = c ^ sw_rope(r).
+__device__ __forceinline__ int sw_kv(int r) {
+    return ((r & 3) << 2) | (((r >> 2) & 1) << 1) | ((r >> 3) & 1);
+}
 __device__ __forceinline__ int sw_rope(int r) { return (r >> 1) & 7; }
-
-__device__ __forceinline__ float wave_max_over_groups(float v) {
-    // lanes l, l^16, l^32, l^48 hold the same head
-    v = fmaxf(v, __shfl_xor(v, 16));
-    v = fmaxf(v, __shfl_xor(v, 32));
-    return v;
-}
-__device__ __forceinline__ float wave_sum_over_groups(float v) {
-    v += __shfl_xor(v, 16);
-    v += __shfl_xor(v, 32);
-    return v;
-}
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// Store 4 consecutive outputs of one head row: bf16 (final) or fp32 (partial).
-__device__ __forceinline__ void store_out4(uint16_t* dst, f32x4 v, float inv_l) {
-    bf16x4 b;
-    b[0] = (__bf16)(v[0] * inv_l);
-    b[1] = (__bf16)(v[1] * inv_l);
-    b[2] = (__bf16)(v[2] * inv_l);
-    b[3] = (__bf16)(v[3] * inv_l);
-    *reinterpret_cast<bf16x4*>(dst) = b;
-}
-
-template <int HW, int KW, int BN, int NSTAGE>
-struct Layout {
-    static constexpr int NW = HW * KW;             // waves per workgroup
-    static constexpr int NT = NW * 64;             // threads
-    static constexpr int RPW = BN / KW;            // tile rows per wave
-    static constexpr int NSUB = RPW / 16;          // 16-row subtiles per wave
-    static constexpr int KV_BYTES = BN * 1024;
-    static constexpr int ROPE_BYTES = BN * 128;
-    static constexpr int STAGE_BYTES = KV_BYTES + ROPE_BYTES;
-    static constexpr int IDX_OFF = NSTAGE * STAGE_BYTES;
-    static constexpr int LDS_BYTES = IDX_OFF + DSA_IDX_CAP * 4;
-    static constexpr int KV_PER_WAVE = BN / NW;    // kv row gathers per wave per tile
-    static constexpr int ROPE_PER_WAVE = BN / 8 / NW;  // rope gathers (8 rows each)
-    static constexpr int LOADS_PER_TILE = KV_PER_WAVE + ROPE_PER_WAVE;
-    // epilogue exchange for KW > 1 (reuses the ring)
-    static constexpr int OX_STRIDE = 516;          // floats per head row (padded)
-    static constexpr int OX_BYTES = NW * 16 * OX_STRIDE * 4;
-    static_assert(BN % (8 * NW) == 0, "rope gathers must split evenly over waves");
-    static_assert(RPW == 16 || RPW == 32 || RPW == 64, "rows per wave");
-    static_assert(LDS_BYTES <= 160 * 1024, "LDS budget");
-    static_assert(KW == 1 || OX_BYTES <= IDX_OFF, "epilogue exchange fits the ring");
-    static_assert(NSTAGE == 2, "ring depth");
+// ------------------------------------------------------------ shared pieces
+struct WgCoords {
+    int token, sp, hgi, b, nt, slot0;
 };
 
-template <int HW, int KW, int BN, int NSTAGE>
-__global__ __launch_bounds__(HW * KW * 64, 1) void sparse_mla_fwd_kernel(FwdParams p) {
-    using C = Layout<HW, KW, BN, NSTAGE>;
-    __shared__ __attribute__((aligned(1024))) char smem[C::LDS_BYTES];
-    const uint32_t lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)smem;
-
-    const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int hw = wave % HW;
-    const int kw = wave / HW;
-    const int g = lane >> 4;
-    const int n16 = lane & 15;
-
-    // ---- workgroup -> (row group = token * nsplit + split, head group).
-    // Workgroups are dispatched round-robin over the 8 XCDs; when possible all
-    // head groups of one row group land on the same XCD so the gathered rows
-    // are fetched from HBM once and re-read from that XCD's L2.
+// Workgroup -> (row group = token * nsplit + split, head group).  Workgroups
+// are dispatched round-robin over the 8 XCDs; when possible all head groups
+// of one row group land on the same XCD so the gathered rows are fetched from
+// HBM once and re-read from that XCD's L2.
+__device__ __forceinline__ WgCoords wg_coords(const FwdParams& p) {
     const int wg = blockIdx.x;
     int rg, hgi;
     if ((p.rowgroups & 7) == 0) {
@@ -170,73 +151,372 @@ __global__ __launch_bounds__(HW * KW * 64, 1) void sparse_mla_fwd_kernel(FwdPara
         rg = wg / p.hgroups;
         hgi = wg % p.hgroups;
     }
-    const int token = rg / p.nsplit;
-    const int sp = rg % p.nsplit;
-    const int b = token / p.SQ;
-    const int head = hgi * (16 * HW) + hw * 16 + n16;  // this lane's head
-    const int t_begin = (int)(((int64_t)sp * p.ntiles) / p.nsplit);
-    const int t_end = (int)(((int64_t)(sp + 1) * p.ntiles) / p.nsplit);
-    const int nt = t_end - t_begin;
-    const int slot0 = t_begin * BN;
-    const int nslots = nt * BN;  // <= DSA_IDX_CAP, checked on the host
+    WgCoords c;
+    c.token = rg / p.nsplit;
+    c.sp = rg % p.nsplit;
+    c.hgi = hgi;
+    c.b = c.token / p.SQ;
+    const int t_begin = (int)(((int64_t)c.sp * p.ntiles) / p.nsplit);
+    const int t_end = (int)(((int64_t)(c.sp + 1) * p.ntiles) / p.nsplit);
+    c.nt = t_end - t_begin;
+    c.slot0 = t_begin * kBN;
+    return c;
+}
+
+// Indices of the workgroup's slot range -> LDS, padded with -1 so a ragged
+// last tile is masked.  nslots <= DSA_IDX_CAP (checked on the host).
+__device__ __forceinline__ void load_indices(const FwdParams& p, const WgCoords& c, uint32_t idx_lds) {
+    const int32_t* gidx = p.idx + (int64_t)c.token * p.TOPK;
+    const int nslots = c.nt * kBN;
+    for (int s = threadIdx.x; s < nslots; s += kThreads) {
+        const int slot = c.slot0 + s;
+        lds_store<int>(idx_lds + 4 * s, slot < p.TOPK ? gidx[slot] : -1);
+    }
+}
+
+// Gather of workgroup tile t into ring stage `stage` (LDS byte address).
+// Wave w fetches kv rows [16w, 16w+16) (1 KiB each, one instruction per row)
+// and rope rows [16w, 16w+16) (8 rows per instruction).
+__device__ __forceinline__ void issue_tile(const FwdParams& p, int t, uint32_t stage, uint32_t idx_lds,
+                                           int64_t kv_batch, int wave, int lane) {
+    const char* kv_base = reinterpret_cast<const char*>(p.kv);
+    const char* kr_base = reinterpret_cast<const char*>(p.k_rope);
+    const int L = p.L;
+    const int r0 = wave * kKvPerWave;
+    const int my_id = lds_load<int>(idx_lds + 4 * (t * kBN + r0 + (lane % kKvPerWave)));
+#pragma unroll
+    for (int rr = 0; rr < kKvPerWave; ++rr) {
+        const int r = r0 + rr;
+        int id = __builtin_amdgcn_readlane(my_id, rr);
+        id = min(max(id, 0), L - 1);  // address clamp; the mask uses the raw index
+        const char* src = kv_base + ((kv_batch + id) << 10) + ((lane ^ sw_kv(r)) << 4);
+        gather16(stage + r * 1024, src);
+    }
+#pragma unroll
+    for (int jj = 0; jj < kRopePerWave; ++jj) {
+        const int j = wave * kRopePerWave + jj;
+        const int r = j * 8 + (lane >> 3);
+        int id = lds_load<int>(idx_lds + 4 * (t * kBN + r));
+        id = min(max(id, 0), L - 1);
+        const char* src = kr_base + ((kv_batch + id) << 7) + (((lane & 7) ^ sw_rope(r)) << 4);
+        gather16(stage + kKvBytes + j * 1024, src);
+    }
+}
+
+// Store 4 consecutive bf16 outputs of one head row.
+__device__ __forceinline__ void store_bf16x4(uint16_t* dst, float a, float b, float c, float d) {
+    bf16x4 v;
+    v[0] = (__bf16)a;
+    v[1] = (__bf16)b;
+    v[2] = (__bf16)c;
+    v[3] = (__bf16)d;
+    *reinterpret_cast<bf16x4*>(dst) = v;
+}
+
+// ====================================================================== wide
+// HW head-waves of 32 heads x KW kv-waves (HW * KW == 4).  Wave (hw, kw)
+// processes rows [kw*RPW, (kw+1)*RPW) of every tile for heads hw*32..+31.
+//
+// 32x32x16 operand layouts (lane i, h = i >> 5, n = i & 31):
+//   A[m = n][k = 8h + j], B[k = 8h + j][n = n], C[m = 8*(r>>2) + 4h + (r&3)][n = n].
+template <int HW, int KW>
+__global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd_wide(FwdParams p) {
+    static_assert(HW * KW == kWaves && (KW == 1 || KW == 2), "wide variant shape");
+    constexpr int RPW = kBN / KW;   // rows per wave per tile
+    constexpr int NSUB = RPW / 32;  // 32-row subtiles per wave per tile
+    __shared__ __attribute__((aligned(1024))) char smem[kLdsBytes];
+    const uint32_t lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)smem;
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int hw = wave % HW;
+    const int kw = wave / HW;
+    const int h = lane >> 5;
+    const int n32 = lane & 31;
+    const int G = lane >> 4;
+    const int n16 = lane & 15;
+
+    const WgCoords c = wg_coords(p);
+    const int head = c.hgi * (32 * HW) + hw * 32 + n32;  // this lane's head
     const int L = p.L;
 
     // ---- Q fragments: B operand of S^T = K . Q^T.  Lane holds
-    // Q[head][32*ks + 8*g .. +7]; ks 16, 17 come from q_rope.
+    // Q[head][16*ks + 8*h .. +7]; ks 32..35 come from q_rope.
+    bf16x8 qf[36];
+    {
+        const uint16_t* qrow = p.q + ((int64_t)c.token * p.H + head) * 512 + 8 * h;
+#pragma unroll
+        for (int ks = 0; ks < 32; ++ks) qf[ks] = *reinterpret_cast<const bf16x8*>(qrow + 16 * ks);
+        const uint16_t* rrow = p.q_rope + ((int64_t)c.token * p.H + head) * 64 + 8 * h;
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) qf[32 + ks] = *reinterpret_cast<const bf16x8*>(rrow + 16 * ks);
+    }
+
+    const uint32_t idx_lds = lds + kIdxOff;
+    load_indices(p, c, idx_lds);
+    lds_barrier();
+    const int64_t kv_batch = (int64_t)c.b * L;
+
+    // ---- per-lane LDS offsets.  Swizzles depend on the row mod 16 and XOR
+    // only the low 4 bits of a chunk index, so every fragment address is a
+    // per-lane base plus a compile-time multiple of 256 bytes.
+    const int rowbase = kw * RPW;
+    // QK A operand: row rowbase + 32*s + n32, logical chunk 2*ks + h =
+    // 16*(ks >> 3) + (2*(ks & 7) + h).
+    uint32_t qk_off[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) qk_off[j] = ((2 * j + h) ^ sw_kv(n32 & 15)) << 4;
+    uint32_t rp_off[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) rp_off[j] = ((2 * j + h) ^ sw_rope(n32 & 15)) << 4;
+    // PV A operand (transposed reads): for k-step kk and read rd, row
+    // rowbase + 32*s + 16*kk + 8*rd + 4*h + n16/4, columns 32*cb + 16*(G&1) +
+    // 4*(n16&3) -> logical chunk 4*cb + 2*(G&1) + ((n16&3)>>1) =
+    // 16*(cb >> 2) + (4*(cb&3) + ...), byte 8*(n16&1) within the chunk.
+    const int tr_row = 4 * h + (n16 >> 2);
+    uint32_t tr_off[2][4];
+#pragma unroll
+    for (int rd = 0; rd < 2; ++rd)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            tr_off[rd][j] = (((4 * j + 2 * (G & 1) + ((n16 & 3) >> 1)) ^ sw_kv(tr_row + 8 * rd)) << 4) +
+                            ((n16 & 1) << 3);
+
+    // ---- running state (log2 units)
+    f32x16 oacc[16];
+    float m_ref = -FLT_MAX;   // reference max of P
+    float m_true = -FLT_MAX;  // exact running max
+    float l_run = 0.f;        // per-lane partial of the head's sum, relative to m_ref
+    const uint32_t flag_lds = lds + kGenOff;
+
+    // At most two passes over the range (see kRestartLog2).  Pass 0 fixes
+    // m_ref at the first tile with a valid row; if any head's max later grows
+    // past m_ref + kRestartLog2, pass 1 recomputes the range with m_ref = the
+    // exact max found by pass 0, which no score can exceed.
+#pragma unroll 1
+    for (int pass = 0; pass < 2; ++pass) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) oacc[i] = f32x16{};
+        l_run = 0.f;
+        if (pass == 1) m_ref = m_true;
+        bool overflow = false;
+        if (c.nt > 0) issue_tile(p, 0, lds, idx_lds, kv_batch, wave, lane);
+
+        for (int t = 0; t < c.nt; ++t) {
+            const int st = t & 1;
+            wait_vmcnt0();
+            lds_barrier();
+            if (t + 1 < c.nt) issue_tile(p, t + 1, lds + (st ^ 1) * kStageBytes, idx_lds, kv_batch, wave, lane);
+            const uint32_t stage = lds + st * kStageBytes;
+
+#pragma unroll
+            for (int s = 0; s < NSUB; ++s) {
+                __builtin_amdgcn_sched_barrier(0);
+                const int row0 = rowbase + 32 * s;
+                // ---- S^T = K . Q^T for rows row0..row0+31.  Explicit 4-deep
+                // software pipeline: fragment ks+4 is read while MFMA ks runs,
+                // and the scheduler is fenced per step so at most 4 fragments
+                // are live.
+                f32x16 sacc = f32x16{};
+                const uint32_t rowa = stage + (row0 + n32) * 1024;
+                const uint32_t rowr = stage + kKvBytes + (row0 + n32) * 128;
+                auto kfrag = [&](int ks) -> bf16x8 {
+                    return ks < 32 ? lds_load<bf16x8>(rowa + qk_off[ks & 7] + ((ks >> 3) << 8))
+                                   : lds_load<bf16x8>(rowr + rp_off[ks - 32]);
+                };
+                bf16x8 kf[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) kf[j] = kfrag(j);
+#pragma unroll
+                for (int ks = 0; ks < 36; ++ks) {
+                    sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[ks & 3], qf[ks], sacc, 0, 0, 0);
+                    if (ks + 4 < 36) kf[ks & 3] = kfrag(ks + 4);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+
+                // ---- scale, mask, online softmax.  Lane holds rows
+                // row0 + 8*q + 4*h + (0..3) for q = 0..3 (register 4q + j) of head n32.
+                float x[16];
+                float mloc = -INFINITY;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const i32x4 iv = lds_load<i32x4>(idx_lds + 4 * (t * kBN + row0 + 8 * q + 4 * h));
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const bool valid = (unsigned)iv[j] < (unsigned)L;
+                        const float v = valid ? sacc[4 * q + j] * kScoreLog2 : -INFINITY;
+                        x[4 * q + j] = v;
+                        mloc = fmaxf(mloc, v);
+                    }
+                }
+                mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
+                m_true = fmaxf(m_true, mloc);
+                if (m_ref == -FLT_MAX) m_ref = m_true;  // first valid rows: O and l are still zero
+                overflow |= m_true > m_ref + kRestartLog2;
+                // P <= 2^kRestartLog2 unless this pass is to be discarded; the
+                // clamp keeps a discarded pass free of inf.
+                bf16x8 pk[2];
+                float psum = 0.f;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const float e = fast_exp2(fminf(x[r] - m_ref, kRestartLog2));
+                    psum += e;
+                    pk[r >> 3][r & 7] = (__bf16)e;
+                }
+                l_run += psum;
+
+                // ---- O^T += V^T . P^T, two k-steps of 16 rows x 16 column
+                // blocks, same 4-deep pipeline over the 32 (kk, cb) steps.
+                const uint32_t vrow = stage + (row0 + tr_row) * 1024;
+                auto vfrag = [&](int step) -> bf16x8 {
+                    const int kk = step >> 4, cb = step & 15;
+                    const uint32_t r0a = vrow + kk * 16 * 1024 + ((cb >> 2) << 8);
+                    const bf16x4 v0 = lds_load_tr(r0a + tr_off[0][cb & 3]);
+                    const bf16x4 v1 = lds_load_tr(r0a + 8 * 1024 + tr_off[1][cb & 3]);
+                    return __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7);
+                };
+                bf16x8 vf[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) vf[j] = vfrag(j);
+#pragma unroll
+                for (int step = 0; step < 32; ++step) {
+                    const int kk = step >> 4, cb = step & 15;
+                    oacc[cb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[step & 3], pk[kk], oacc[cb], 0, 0, 0);
+                    if (step + 4 < 32) vf[step & 3] = vfrag(step + 4);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            }
+        }
+        // ---- workgroup vote: does any head need pass 1?
+        if (pass == 1) break;
+        if (threadIdx.x == 0) lds_store<int>(flag_lds, 0);
+        lds_barrier();  // also: every wave is past its last ring read
+        if (__any(overflow) && lane == 0) lds_store<int>(flag_lds, 1);
+        lds_barrier();
+        if (__builtin_amdgcn_readfirstlane(lds_load<int>(flag_lds)) == 0) break;
+    }
+
+    // ---- epilogue
+    l_run += __shfl_xor(l_run, 32);
+    if constexpr (KW == 2) {
+        // kv-wave 1 hands (m_ref, m_true, l, O) to kv-wave 0 of the same head
+        // slice through LDS; kv-wave 0 merges (m = max, w = exp(m_k - m)).
+        constexpr int OX_STRIDE = 516;  // floats per head row, padded
+        static_assert(2 * 32 * OX_STRIDE * 4 <= kIdxOff, "exchange fits the ring");
+        lds_barrier();                  // every wave is past its last ring read
+        const uint32_t ml = lds + kIdxOff;
+        const uint32_t ox = lds + ((hw * 32 + n32) * OX_STRIDE + 4 * h) * 4;
+        if (kw == 1) {
+            if (h == 0) {
+                lds_store<float>(ml + 4 * (hw * 32 + n32), m_ref);
+                lds_store<float>(ml + 4 * (64 + hw * 32 + n32), m_true);
+                lds_store<float>(ml + 4 * (128 + hw * 32 + n32), l_run);
+            }
+#pragma unroll
+            for (int cb = 0; cb < 16; ++cb)
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    lds_store<f32x4>(ox + (32 * cb + 8 * q) * 4,
+                                     f32x4{oacc[cb][4 * q], oacc[cb][4 * q + 1], oacc[cb][4 * q + 2],
+                                           oacc[cb][4 * q + 3]});
+        }
+        lds_barrier();
+        if (kw == 1) return;
+        const float m1 = lds_load<float>(ml + 4 * (hw * 32 + n32));
+        const float t1 = lds_load<float>(ml + 4 * (64 + hw * 32 + n32));
+        const float l1 = lds_load<float>(ml + 4 * (128 + hw * 32 + n32));
+        const float mm = fmaxf(m_ref, m1);
+        const float w0 = fast_exp2(m_ref - mm), w1 = fast_exp2(m1 - mm);
+        l_run = w0 * l_run + w1 * l1;
+        m_ref = mm;
+        m_true = fmaxf(m_true, t1);
+#pragma unroll
+        for (int cb = 0; cb < 16; ++cb)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const f32x4 v = lds_load<f32x4>(ox + (32 * cb + 8 * q) * 4);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) oacc[cb][4 * q + j] = w0 * oacc[cb][4 * q + j] + w1 * v[j];
+            }
+    }
+
+    // Re-express (m_ref, l, O) against the true max for the caller.
+    const float to_true = fast_exp2(m_ref - m_true);
+    const float l_fin = l_run * to_true;
+    const float m_nat = m_true * kLn2;
+    if (p.nsplit == 1) {
+        const float inv_l = 1.0f / l_run;  // O and l_run share m_ref
+        uint16_t* orow = p.out + ((int64_t)c.token * p.H + head) * 512 + 4 * h;
+#pragma unroll
+        for (int cb = 0; cb < 16; ++cb)
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                store_bf16x4(orow + 32 * cb + 8 * q, oacc[cb][4 * q] * inv_l, oacc[cb][4 * q + 1] * inv_l,
+                             oacc[cb][4 * q + 2] * inv_l, oacc[cb][4 * q + 3] * inv_l);
+        if (h == 0) {
+            p.out_max[(int64_t)c.token * p.H + head] = m_nat;
+            p.out_sum[(int64_t)c.token * p.H + head] = l_fin;
+        }
+    } else {
+        const int64_t prow = ((int64_t)c.token * p.nsplit + c.sp) * p.H + head;
+        float* orow = p.part_o + prow * 512 + 4 * h;
+#pragma unroll
+        for (int cb = 0; cb < 16; ++cb)
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                *reinterpret_cast<f32x4*>(orow + 32 * cb + 8 * q) =
+                    f32x4{oacc[cb][4 * q], oacc[cb][4 * q + 1], oacc[cb][4 * q + 2], oacc[cb][4 * q + 3]} *
+                    to_true;
+        if (h == 0) {
+            p.part_m[prow] = m_nat;
+            p.part_l[prow] = l_fin;
+        }
+    }
+}
+
+// ==================================================================== narrow
+// HW head-waves of 16 heads x KW kv-waves (HW * KW == 4).
+//
+// 16x16x32 operand layouts (lane i, g = i >> 4, n = i & 15):
+//   A[m = n][k = 8g + j], B[k = 8g + j][n = n], C[m = 4g + r][n = n].
+template <int HW, int KW>
+__global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd_narrow(FwdParams p) {
+    static_assert(HW * KW == kWaves, "narrow variant shape");
+    constexpr int RPW = kBN / KW;   // tile rows per wave
+    constexpr int NSUB = RPW / 16;  // 16-row subtiles per wave
+    static_assert(RPW == 16 || RPW == 32 || RPW == 64, "rows per wave");
+    __shared__ __attribute__((aligned(1024))) char smem[kLdsBytes];
+    const uint32_t lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)smem;
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int hw = wave % HW;
+    const int kw = wave / HW;
+    const int g = lane >> 4;
+    const int n16 = lane & 15;
+
+    const WgCoords c = wg_coords(p);
+    const int head = c.hgi * (16 * HW) + hw * 16 + n16;  // this lane's head
+    const int L = p.L;
+
+    // ---- Q fragments: lane holds Q[head][32*ks + 8*g .. +7]; ks 16, 17 from q_rope.
     bf16x8 qf[18];
     {
-        const uint16_t* qrow = p.q + ((int64_t)token * p.H + head) * 512 + 8 * g;
+        const uint16_t* qrow = p.q + ((int64_t)c.token * p.H + head) * 512 + 8 * g;
 #pragma unroll
         for (int ks = 0; ks < 16; ++ks) qf[ks] = *reinterpret_cast<const bf16x8*>(qrow + 32 * ks);
-        const uint16_t* rrow = p.q_rope + ((int64_t)token * p.H + head) * 64 + 8 * g;
+        const uint16_t* rrow = p.q_rope + ((int64_t)c.token * p.H + head) * 64 + 8 * g;
         qf[16] = *reinterpret_cast<const bf16x8*>(rrow);
         qf[17] = *reinterpret_cast<const bf16x8*>(rrow + 32);
     }
 
-    // ---- indices of this workgroup's slot range -> LDS, padded with -1 so a
-    // ragged last tile is masked.
-    const uint32_t idx_lds = lds + C::IDX_OFF;
-    {
-        const int32_t* gidx = p.idx + (int64_t)token * p.TOPK;
-        for (int s = threadIdx.x; s < nslots; s += C::NT) {
-            const int slot = slot0 + s;
-            lds_store<int>(idx_lds + 4 * s, slot < p.TOPK ? gidx[slot] : -1);
-        }
-    }
+    const uint32_t idx_lds = lds + kIdxOff;
+    load_indices(p, c, idx_lds);
     lds_barrier();
+    const int64_t kv_batch = (int64_t)c.b * L;
 
-    const int64_t kv_batch = (int64_t)b * L;
-    const char* kv_base = reinterpret_cast<const char*>(p.kv);
-    const char* kr_base = reinterpret_cast<const char*>(p.k_rope);
-
-    // ---- gather of tile t (workgroup-local index) into ring stage st.
-    auto issue_tile = [&](int t, int st) {
-        const uint32_t stage = lds + st * C::STAGE_BYTES;
-        const int r0 = wave * C::KV_PER_WAVE;
-        const int my_id = lds_load<int>(idx_lds + 4 * (t * BN + r0 + (lane % C::KV_PER_WAVE)));
-#pragma unroll
-        for (int rr = 0; rr < C::KV_PER_WAVE; ++rr) {
-            const int r = r0 + rr;
-            int id = __builtin_amdgcn_readlane(my_id, rr);
-            id = min(max(id, 0), L - 1);  // address clamp; the mask uses the raw index
-            const char* src = kv_base + ((kv_batch + id) << 10) + ((lane ^ sw_kv(r)) << 4);
-            gather16(stage + r * 1024, src);
-        }
-#pragma unroll
-        for (int jj = 0; jj < C::ROPE_PER_WAVE; ++jj) {
-            const int j = wave * C::ROPE_PER_WAVE + jj;
-            const int r = j * 8 + (lane >> 3);
-            int id = lds_load<int>(idx_lds + 4 * (t * BN + r));
-            id = min(max(id, 0), L - 1);
-            const char* src = kr_base + ((kv_batch + id) << 7) + (((lane & 7) ^ sw_rope(r)) << 4);
-            gather16(stage + C::KV_BYTES + j * 1024, src);
-        }
-    };
-
-    // ---- per-lane LDS offsets.  The swizzles depend only on the row mod 16,
-    // and XOR-ing a chunk index only touches its low 4 bits, so every fragment
-    // address is a per-lane base plus a compile-time multiple of 256 bytes.
-    const int rowbase = kw * C::RPW;
+    // ---- per-lane LDS offsets (see the wide variant).
+    const int rowbase = kw * RPW;
     // QK A operand: row rowbase + 16*s + n16, logical chunk 4*ks + g = 16*(ks>>2) + (4*(ks&3) + g)
     uint32_t qk_off[4];
 #pragma unroll
@@ -244,7 +524,7 @@ __global__ __launch_bounds__(HW * KW * 64, 1) void sparse_mla_fwd_kernel(FwdPara
     uint32_t rp_off[2];
 #pragma unroll
     for (int j = 0; j < 2; ++j) rp_off[j] = ((4 * j + g) ^ sw_rope(n16)) << 4;
-    // PV A operand (transposed read): row rowbase + 32*k + 16*h + 4*g + n16/4,
+    // PV A operand (transposed read): row rowbase + 32*k + 16*rd + 4*g + n16/4,
     // column 16*cb + 4*(n16 & 3) -> logical chunk 2*cb + ((n16 & 3) >> 1) =
     // 16*(cb>>3) + (2*(cb&7) + ((n16 & 3) >> 1)), byte 8*(n16 & 1) within it.
     const int tr_row = 4 * g + (n16 >> 2);
@@ -252,32 +532,27 @@ __global__ __launch_bounds__(HW * KW * 64, 1) void sparse_mla_fwd_kernel(FwdPara
 #pragma unroll
     for (int j = 0; j < 8; ++j) tr_off[j] = (((2 * j + ((n16 & 3) >> 1)) ^ sw_kv(tr_row)) << 4) + ((n16 & 1) << 3);
 
-    // ---- running state (log2 units).  P is formed against a reference max
-    // m_ref that only moves when the true running max exceeds it by more than
-    // kRescaleLog2 (then O and l are rescaled); m_true is the exact running
-    // max reported to the caller.  P <= 2^kRescaleLog2, so bf16 P keeps its
-    // relative precision and nothing overflows.
-    constexpr float kRescaleLog2 = 8.0f;
+    // ---- running state (log2 units; see kRescaleLog2)
     f32x4 oacc[32];
 #pragma unroll
     for (int i = 0; i < 32; ++i) oacc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
     float m_ref = -FLT_MAX;
     float m_true = -FLT_MAX;
-    float l_run = 0.f;  // per-lane partial of the head's sum, relative to m_ref
+    float l_run = 0.f;
 
-    if (nt > 0) issue_tile(0, 0);
+    if (c.nt > 0) issue_tile(p, 0, lds, idx_lds, kv_batch, wave, lane);
 
-    for (int t = 0; t < nt; ++t) {
+    for (int t = 0; t < c.nt; ++t) {
         const int st = t & 1;
-        wait_vmcnt<0>();
+        wait_vmcnt0();
         lds_barrier();
-        if (t + 1 < nt) issue_tile(t + 1, st ^ 1);
+        if (t + 1 < c.nt) issue_tile(p, t + 1, lds + (st ^ 1) * kStageBytes, idx_lds, kv_batch, wave, lane);
 
-        const uint32_t stage = lds + st * C::STAGE_BYTES;
+        const uint32_t stage = lds + st * kStageBytes;
         // ---- S^T = K . Q^T for this wave's rows
-        f32x4 sacc[C::NSUB];
+        f32x4 sacc[NSUB];
 #pragma unroll
-        for (int s = 0; s < C::NSUB; ++s) {
+        for (int s = 0; s < NSUB; ++s) {
             sacc[s] = f32x4{0.f, 0.f, 0.f, 0.f};
             const uint32_t rowa = stage + (rowbase + 16 * s + n16) * 1024;
 #pragma unroll
@@ -285,7 +560,7 @@ __global__ __launch_bounds__(HW * KW * 64, 1) void sparse_mla_fwd_kernel(FwdPara
                 const bf16x8 a = lds_load<bf16x8>(rowa + qk_off[ks & 3] + ((ks >> 2) << 8));
                 sacc[s] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qf[ks], sacc[s], 0, 0, 0);
             }
-            const uint32_t rowr = stage + C::KV_BYTES + (rowbase + 16 * s + n16) * 128;
+            const uint32_t rowr = stage + kKvBytes + (rowbase + 16 * s + n16) * 128;
 #pragma unroll
             for (int ks = 0; ks < 2; ++ks) {
                 const bf16x8 a = lds_load<bf16x8>(rowr + rp_off[ks]);
@@ -297,11 +572,11 @@ __global__ __launch_bounds__(HW * KW * 64, 1) void sparse_mla_fwd_kernel(FwdPara
 
         // ---- scale, mask, online softmax.  Lane holds rows
         // rowbase + 16*s + 4*g + r (r = 0..3) of head n16.
-        float x[C::NSUB][4];
+        float x[NSUB][4];
         float mloc = -INFINITY;
 #pragma unroll
-        for (int s = 0; s < C::NSUB; ++s) {
-            const i32x4 iv = lds_load<i32x4>(idx_lds + 4 * (t * BN + rowbase + 16 * s + 4 * g));
+        for (int s = 0; s < NSUB; ++s) {
+            const i32x4 iv = lds_load<i32x4>(idx_lds + 4 * (t * kBN + rowbase + 16 * s + 4 * g));
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const bool valid = (unsigned)iv[r] < (unsigned)L;
@@ -310,7 +585,9 @@ __global__ __launch_bounds__(HW * KW * 64, 1) void sparse_mla_fwd_kernel(FwdPara
                 mloc = fmaxf(mloc, v);
             }
         }
-        m_true = fmaxf(m_true, wave_max_over_groups(mloc));
+        mloc = fmaxf(mloc, __shfl_xor(mloc, 16));
+        mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
+        m_true = fmaxf(m_true, mloc);
         const bool need = m_true > m_ref + kRescaleLog2;
         if (__any(need)) {
             const float nref = need ? m_true : m_ref;
@@ -321,9 +598,9 @@ __global__ __launch_bounds__(HW * KW * 64, 1) void sparse_mla_fwd_kernel(FwdPara
             for (int i = 0; i < 32; ++i) oacc[i] *= alpha;
         }
         float psum = 0.f;
-        bf16x4 pb[C::NSUB];
+        bf16x4 pb[NSUB];
 #pragma unroll
-        for (int s = 0; s < C::NSUB; ++s) {
+        for (int s = 0; s < NSUB; ++s) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const float e = fast_exp2(x[s][r] - m_ref);
@@ -334,9 +611,9 @@ __global__ __launch_bounds__(HW * KW * 64, 1) void sparse_mla_fwd_kernel(FwdPara
         l_run += psum;
 
         // ---- O^T += V^T . P^T
-        if constexpr (C::NSUB >= 2) {
+        if constexpr (NSUB >= 2) {
 #pragma unroll
-            for (int k = 0; k < C::NSUB / 2; ++k) {
+            for (int k = 0; k < NSUB / 2; ++k) {
                 const bf16x8 pk = __builtin_shufflevector(pb[2 * k], pb[2 * k + 1], 0, 1, 2, 3, 4, 5, 6, 7);
                 const uint32_t r0a = stage + (rowbase + 32 * k + tr_row) * 1024;
                 const uint32_t r1a = r0a + 16 * 1024;
@@ -364,20 +641,23 @@ __global__ __launch_bounds__(HW * KW * 64, 1) void sparse_mla_fwd_kernel(FwdPara
     }
 
     // ---- epilogue
-    l_run = wave_sum_over_groups(l_run);
+    l_run += __shfl_xor(l_run, 16);
+    l_run += __shfl_xor(l_run, 32);
     int cb_lo = 0, cb_hi = 32;
 
     if constexpr (KW > 1) {
         // Merge the KW row-split waves of each head slice through LDS (same
         // FP32 merge as the split merge): M = max m_ref_k, w_k = exp(m_ref_k - M).
+        constexpr int OX_STRIDE = 516;  // floats per head row (padded)
+        static_assert(kWaves * 16 * OX_STRIDE * 4 <= kIdxOff, "exchange fits the ring");
         lds_barrier();  // every wave is past its last ring read
-        const uint32_t ml = lds + C::IDX_OFF;  // [3][NW][16] floats: m_ref, m_true, l
+        const uint32_t ml = lds + kIdxOff;  // [3][4 waves][16] floats: m_ref, m_true, l
         if (g == 0) {
             lds_store<float>(ml + 4 * (wave * 16 + n16), m_ref);
-            lds_store<float>(ml + 4 * (C::NW * 16 + wave * 16 + n16), m_true);
-            lds_store<float>(ml + 4 * (2 * C::NW * 16 + wave * 16 + n16), l_run);
+            lds_store<float>(ml + 4 * (kWaves * 16 + wave * 16 + n16), m_true);
+            lds_store<float>(ml + 4 * (2 * kWaves * 16 + wave * 16 + n16), l_run);
         }
-        const uint32_t ox = lds + ((wave * 16 + n16) * C::OX_STRIDE + 4 * g) * 4;
+        const uint32_t ox = lds + ((wave * 16 + n16) * OX_STRIDE + 4 * g) * 4;
 #pragma unroll
         for (int cb = 0; cb < 32; ++cb) lds_store<f32x4>(ox + cb * 64, oacc[cb]);
         lds_barrier();
@@ -387,8 +667,8 @@ __global__ __launch_bounds__(HW * KW * 64, 1) void sparse_mla_fwd_kernel(FwdPara
         for (int k = 0; k < KW; ++k) {
             const int wk = k * HW + hw;
             mk[k] = lds_load<float>(ml + 4 * (wk * 16 + n16));
-            mtrue = fmaxf(mtrue, lds_load<float>(ml + 4 * (C::NW * 16 + wk * 16 + n16)));
-            lk[k] = lds_load<float>(ml + 4 * (2 * C::NW * 16 + wk * 16 + n16));
+            mtrue = fmaxf(mtrue, lds_load<float>(ml + 4 * (kWaves * 16 + wk * 16 + n16)));
+            lk[k] = lds_load<float>(ml + 4 * (2 * kWaves * 16 + wk * 16 + n16));
             mref = fmaxf(mref, mk[k]);
         }
         float lsum = 0.f;
@@ -411,8 +691,7 @@ __global__ __launch_bounds__(HW * KW * 64, 1) void sparse_mla_fwd_kernel(FwdPara
 #pragma unroll
                 for (int k = 0; k < KW; ++k) {
                     const int wk = k * HW + hw;
-                    const f32x4 v =
-                        lds_load<f32x4>(lds + ((wk * 16 + n16) * C::OX_STRIDE + 4 * g + cb * 16) * 4);
+                    const f32x4 v = lds_load<f32x4>(lds + ((wk * 16 + n16) * OX_STRIDE + 4 * g + cb * 16) * 4);
                     acc += wgt[k] * v;
                 }
                 oacc[cb] = acc;
@@ -423,20 +702,21 @@ __global__ __launch_bounds__(HW * KW * 64, 1) void sparse_mla_fwd_kernel(FwdPara
     // Re-express (m_ref, l, O) against the true max for the caller.
     const float to_true = fast_exp2(m_ref - m_true);
     const float l_fin = l_run * to_true;
-    const float m_fin = m_true;
-    const float m_nat = m_fin * kLn2;
+    const float m_nat = m_true * kLn2;
     if (p.nsplit == 1) {
         const float inv_l = 1.0f / l_run;  // O and l_run share m_ref
-        uint16_t* orow = p.out + ((int64_t)token * p.H + head) * 512 + 4 * g;
+        uint16_t* orow = p.out + ((int64_t)c.token * p.H + head) * 512 + 4 * g;
 #pragma unroll
         for (int cb = 0; cb < 32; ++cb)
-            if (cb >= cb_lo && cb < cb_hi) store_out4(orow + 16 * cb, oacc[cb], inv_l);
+            if (cb >= cb_lo && cb < cb_hi)
+                store_bf16x4(orow + 16 * cb, oacc[cb][0] * inv_l, oacc[cb][1] * inv_l, oacc[cb][2] * inv_l,
+                             oacc[cb][3] * inv_l);
         if (g == 0 && kw == 0) {
-            p.out_max[(int64_t)token * p.H + head] = m_nat;
-            p.out_sum[(int64_t)token * p.H + head] = l_fin;
+            p.out_max[(int64_t)c.token * p.H + head] = m_nat;
+            p.out_sum[(int64_t)c.token * p.H + head] = l_fin;
         }
     } else {
-        const int64_t prow = ((int64_t)token * p.nsplit + sp) * p.H + head;
+        const int64_t prow = ((int64_t)c.token * p.nsplit + c.sp) * p.H + head;
         float* orow = p.part_o + prow * 512 + 4 * g;
 #pragma unroll
         for (int cb = 0; cb < 32; ++cb)
@@ -448,31 +728,29 @@ __global__ __launch_bounds__(HW * KW * 64, 1) void sparse_mla_fwd_kernel(FwdPara
     }
 }
 
-template <int HW, int KW, int BN, int NSTAGE>
-int launch_variant(const FwdParams& p, hipStream_t stream) {
-    using C = Layout<HW, KW, BN, NSTAGE>;
-    const int64_t grid = fwd_grid(p);
-    hipLaunchKernelGGL((sparse_mla_fwd_kernel<HW, KW, BN, NSTAGE>), dim3((unsigned)grid), dim3(C::NT), 0,
-                       stream, p);
+template <typename K>
+int launch(K kernel, const FwdParams& p, hipStream_t stream) {
+    hipLaunchKernelGGL(kernel, dim3((unsigned)fwd_grid(p)), dim3(kThreads), 0, stream, p);
     return (int)hipGetLastError();
 }
 
 }  // namespace
 
-bool fwd_variant_exists(int hpg, int kvw, int bn, int stages) {
-    if (bn != 64 || stages != 2) return false;
-    return (hpg == 64 && kvw == 1) || (hpg == 32 && kvw == 2) || (hpg == 16 && kvw == 4);
+bool fwd_variant_exists(int hpg, int kvw, int bn, int stages, int mfma) {
+    if (bn != kBN || stages != 2) return false;
+    if (mfma == 32) return hpg == 64 && kvw == 2;
+    if (mfma == 16) return (hpg == 64 && kvw == 1) || (hpg == 32 && kvw == 2) || (hpg == 16 && kvw == 4);
+    return false;
 }
 
 int64_t fwd_grid(const FwdParams& p) { return (int64_t)p.rowgroups * p.hgroups; }
 
-int launch_fwd(const FwdParams& p, int hpg, int kvw, int bn, int stages, hipStream_t stream) {
-    if (bn == 64 && stages == 2) {
-        if (hpg == 64 && kvw == 1) return launch_variant<4, 1, 64, 2>(p, stream);
-        if (hpg == 32 && kvw == 2) return launch_variant<2, 2, 64, 2>(p, stream);
-        if (hpg == 16 && kvw == 4) return launch_variant<1, 4, 64, 2>(p, stream);
-    }
-    return (int)hipErrorInvalidValue;
+int launch_fwd(const FwdParams& p, int hpg, int kvw, int bn, int stages, int mfma, hipStream_t stream) {
+    if (!fwd_variant_exists(hpg, kvw, bn, stages, mfma)) return (int)hipErrorInvalidValue;
+    if (mfma == 32) return launch(sparse_mla_fwd_wide<2, 2>, p, stream);
+    if (hpg == 64) return launch(sparse_mla_fwd_narrow<4, 1>, p, stream);
+    if (hpg == 32) return launch(sparse_mla_fwd_narrow<2, 2>, p, stream);
+    return launch(sparse_mla_fwd_narrow<1, 4>, p, stream);
 }
 
 }  // namespace dsa

@@ -47,12 +47,15 @@ extern "C" {
  * Launch plan of one call.  Replaces dsa.Tuning (dsa/config.py:10-19), whose
  * fields were Ascend-specific (BM, BN, split, direct_nz, pv_cols, share_score).
  *
- *   heads_per_group : query heads one workgroup owns (16, 32 or 64; divides H)
+ *   heads_per_group : query heads one workgroup owns; divides H
  *   tile_rows       : gathered rows per LDS ring stage (64)
  *   split           : KV splits per (token, head group); > 1 adds the FP32 merge
  *   kv_waves        : waves that share a head slice and split each tile's rows
- *                     (heads_per_group / 16 * kv_waves == 4)
+ *                     (heads_per_group / mfma * kv_waves == 4)
  *   stages          : LDS ring depth (2)
+ *   mfma            : heads per wave = MFMA block: 32 (v_mfma_f32_32x32x16_bf16;
+ *                     heads_per_group 64, kv_waves 2) or 16 (v_mfma_f32_16x16x32_bf16;
+ *                     heads_per_group 64, 32 or 16)
  */
 typedef struct dsa_plan {
     int32_t heads_per_group;
@@ -60,7 +63,8 @@ typedef struct dsa_plan {
     int32_t split;
     int32_t kv_waves;
     int32_t stages;
-    int32_t reserved[3];
+    int32_t mfma;
+    int32_t reserved[2];
 } dsa_plan;
 
 /* Library version, (major << 16) | minor. */

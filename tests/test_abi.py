@@ -69,7 +69,7 @@ def test_fwd_and_merge_validate_before_any_launch():
 
 def test_partial_elems():
     lib = _lib.load()
-    plan = _lib.DsaPlan(64, 64, 4, 1, 2)
+    plan = _lib.DsaPlan(64, 64, 4, 2, 2, 32)
     o, ml = ctypes.c_int64(), ctypes.c_int64()
     assert lib.dsa_partial_elems(ctypes.byref(plan), 8, 1, 128, ctypes.byref(o), ctypes.byref(ml)) == 0
     assert (o.value, ml.value) == (8 * 4 * 128 * 512, 8 * 4 * 128)
@@ -81,5 +81,5 @@ def test_partial_elems():
 @pytest.mark.parametrize("split", [1, 3, 32])
 def test_plan_check_accepts_valid(split):
     lib = _lib.load()
-    plan = _lib.DsaPlan(64, 64, split, 1, 2)
+    plan = _lib.DsaPlan(64, 64, split, 2, 2, 32)
     assert lib.dsa_plan_check(ctypes.byref(plan), 1, 1, 128, 8192, 2048) == 0

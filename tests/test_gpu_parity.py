@@ -114,9 +114,11 @@ def test_c5_sampled_tokens_per_family():
 
 
 # ------------------------------------------------------- plans, edges, invariants
-PLANS_H128 = [Tuning(64, 64, 1), Tuning(64, 64, 2), Tuning(64, 64, 7), Tuning(64, 64, 32),
-              Tuning(32, 64, 1, kv_waves=2), Tuning(32, 64, 5, kv_waves=2),
-              Tuning(16, 64, 1, kv_waves=4), Tuning(16, 64, 32, kv_waves=4)]
+PLANS_H128 = [Tuning(64, 64, 1, kv_waves=2), Tuning(64, 64, 2, kv_waves=2), Tuning(64, 64, 7, kv_waves=2),
+              Tuning(64, 64, 32, kv_waves=2),
+              Tuning(64, 64, 1, mfma=16), Tuning(64, 64, 32, mfma=16),
+              Tuning(32, 64, 1, kv_waves=2, mfma=16), Tuning(32, 64, 5, kv_waves=2, mfma=16),
+              Tuning(16, 64, 1, kv_waves=4, mfma=16), Tuning(16, 64, 32, kv_waves=4, mfma=16)]
 
 
 @pytest.mark.parametrize("config", PLANS_H128, ids=str)

@@ -88,7 +88,7 @@ def test_planner_covers_any_shape(shape):
     ntiles = -(-topk // plan.bn)
     assert 1 <= plan.split <= ntiles
     assert -(-ntiles // plan.split) * plan.bn <= 2048  # index cache of one workgroup
-    assert shape[2] % plan.bm == 0 and plan.bm // 16 * plan.kv_waves == 4
+    assert shape[2] % plan.bm == 0 and plan.bm // plan.mfma * plan.kv_waves == 4
 
 
 def test_plan_call_allocations_and_launches():
@@ -104,7 +104,7 @@ def test_plan_call_allocations_and_launches():
 
 def test_plan_call_explicit_tuning_and_errors():
     shape = (1, 1, 128, 8192, 2048)
-    config, partials, _ = plan_call(shape, Tuning(32, 64, 4, kv_waves=2))
+    config, partials, _ = plan_call(shape, Tuning(32, 64, 4, kv_waves=2, mfma=16))
     assert config.split == 4 and partials[0][2] == 4
     with pytest.raises(ValueError):
         plan_call(shape, cores=0)
@@ -113,13 +113,16 @@ def test_plan_call_explicit_tuning_and_errors():
 
 
 TUNING_MUTATIONS = {
-    "bm not dividing H": Tuning(64, 64, 1),
-    "bm 48": Tuning(48, 64, 1),
-    "bn 128": Tuning(16, 128, 1, kv_waves=4),
-    "split 0": Tuning(16, 64, 0, kv_waves=4),
-    "split > tiles": Tuning(16, 64, 2, kv_waves=4),
-    "kv_waves mismatch": Tuning(16, 64, 1, kv_waves=1),
-    "stages 3": Tuning(16, 64, 1, kv_waves=4, stages=3),
+    "bm not dividing H": Tuning(64, 64, 1, kv_waves=2),
+    "bm 48": Tuning(48, 64, 1, mfma=16),
+    "bn 128": Tuning(16, 128, 1, kv_waves=4, mfma=16),
+    "split 0": Tuning(16, 64, 0, kv_waves=4, mfma=16),
+    "split > tiles": Tuning(16, 64, 2, kv_waves=4, mfma=16),
+    "kv_waves mismatch": Tuning(16, 64, 1, kv_waves=1, mfma=16),
+    "stages 3": Tuning(16, 64, 1, kv_waves=4, stages=3, mfma=16),
+    "mfma 8": Tuning(16, 64, 1, kv_waves=4, mfma=8),
+    "wide with 16 heads": Tuning(16, 64, 1, kv_waves=4, mfma=32),
+    "wide 128 heads": Tuning(128, 64, 1, kv_waves=1, mfma=32),
 }
 
 
@@ -140,5 +143,5 @@ def test_tuning_type_error():
 def test_index_cache_limit_forces_split():
     # TOPK 8192 = 128 tiles; one workgroup holds at most 2048 slots -> split >= 4
     with pytest.raises(ValueError):
-        check_tuning(Tuning(64, 64, 2), (1, 1, 64, 100000, 8192))
-    check_tuning(Tuning(64, 64, 4), (1, 1, 64, 100000, 8192))
+        check_tuning(Tuning(64, 64, 2, kv_waves=2), (1, 1, 64, 100000, 8192))
+    check_tuning(Tuning(64, 64, 4, kv_waves=2), (1, 1, 64, 100000, 8192))
