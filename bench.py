@@ -169,8 +169,10 @@ def run(name, args):
     rotate = args.rotate if args.rotate else DEFAULT_ROTATE[name]
     config = dsa_amd.select(shape)
     if args.plan:
-        bm, split, kv_waves, mfma = (int(v) for v in args.plan.split(","))
-        config = Tuning(bm, 64, split, kv_waves=kv_waves, mfma=mfma)
+        v = [int(x) for x in args.plan.split(",")]
+        bm, split, kv_waves, mfma = v[:4]
+        bn, stages = (v[4], v[5]) if len(v) > 4 else (64, 2)
+        config = Tuning(bm, bn, split, kv_waves=kv_waves, stages=stages, mfma=mfma)
     print(f"[bench] {name} shape={shape} plan={config} rotate={rotate}", file=sys.stderr, flush=True)
     sets = [baseline_inputs(name, seed=args.seed + i, device="cuda", cpu_recipe=False) for i in range(rotate)]
     calls = [Call(d, config) for d in sets]
@@ -230,7 +232,7 @@ def main():
     ap.add_argument("--config", default="c2_decode_b8", choices=sorted(BASELINE_CONFIGS))
     ap.add_argument("--all", action="store_true", help="one line per configuration C2..C5")
     ap.add_argument("--rotate", type=int, default=0, help="input sets to cycle (default per workload)")
-    ap.add_argument("--plan", default="", help="override the plan: bm,split,kv_waves,mfma")
+    ap.add_argument("--plan", default="", help="override the plan: bm,split,kv_waves,mfma[,bn,stages]")
     ap.add_argument("--seed", type=int, default=20261102)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU oracle timing")

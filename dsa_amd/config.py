@@ -5,13 +5,14 @@ SELECTED :42-59, select :64-69).  The reference's Tuning fields described an
 Ascend Cube/Vector pipeline; here the plan describes gfx950 workgroups:
 
 * ``bm``       -- query heads per workgroup (divides H);
-* ``bn``       -- gathered rows per LDS ring stage (64);
+* ``bn``       -- gathered rows per LDS ring stage (32 or 64);
 * ``split``    -- KV splits per (token, head group); > 1 adds the FP32 merge;
 * ``kv_waves`` -- waves that share a head slice and split each tile's rows
                   (``bm // mfma * kv_waves == 4``: four waves per workgroup);
-* ``stages``   -- LDS ring depth (2);
-* ``mfma``     -- heads per wave: 32 (v_mfma_f32_32x32x16_bf16, bm 64 with
-                  kv_waves 2) or 16 (v_mfma_f32_16x16x32_bf16, bm 64, 32 or 16).
+* ``stages``   -- LDS ring depth (2 or 4);
+* ``mfma``     -- heads per wave: 32 (v_mfma_f32_32x32x16_bf16: bm 128 with
+                  bn 32 and 4 stages, or bm 64 with kv_waves 2) or 16
+                  (v_mfma_f32_16x16x32_bf16: bm 64, 32 or 16, bn 64, 2 stages).
 
 Unlike the reference, shapes outside the table are accepted: the library's
 planner (``dsa_plan_for``) derives a plan for any supported shape.
@@ -100,30 +101,31 @@ def check_tuning(config: Tuning, shape) -> None:
 
 # Per-shape plans for MI355X (256 CUs), re-derived from the reference's table
 # (dsa/config.py:42-59) for gfx950: four waves per workgroup, one 152 KiB
-# workgroup per CU, 32-head waves wherever H is a multiple of 64, KV split
-# until the grid covers the CUs.
+# workgroup per CU, 32-head waves wherever H is a multiple of 64 (128-head
+# workgroups when H is a multiple of 128), KV split until the grid covers the
+# CUs.
 SELECTED = {
-    "decode_b1": Tuning(64, 64, 32, kv_waves=2),
-    "decode_b8": Tuning(64, 64, 16, kv_waves=2),
-    "decode_b32": Tuning(64, 64, 4, kv_waves=2),
+    "decode_b1": Tuning(128, 32, 64, stages=4),
+    "decode_b8": Tuning(32, 64, 8, kv_waves=2, mfma=16),
+    "decode_b32": Tuning(128, 32, 8, stages=4),
     "decode_tp8": Tuning(16, 64, 32, kv_waves=4, mfma=16),
-    "prefill_q16": Tuning(64, 64, 8, kv_waves=2),
-    "prefill_q64": Tuning(64, 64, 2, kv_waves=2),
+    "prefill_q16": Tuning(128, 32, 16, stages=4),
+    "prefill_q64": Tuning(128, 32, 4, stages=4),
     "prefill_tp8": Tuning(16, 64, 2, kv_waves=4, mfma=16),
     "prefill_k512": Tuning(64, 64, 2, kv_waves=2),
-    "decode_b4_h128": Tuning(64, 64, 32, kv_waves=2),
-    "prefill_b4_h128": Tuning(64, 64, 1, kv_waves=2),
+    "decode_b4_h128": Tuning(128, 32, 64, stages=4),
+    "prefill_b4_h128": Tuning(128, 32, 1, stages=4),
     "decode_b4_h64": Tuning(64, 64, 32, kv_waves=2),
     "prefill_b4_h64": Tuning(64, 64, 1, kv_waves=2),
     "decode_b4_h32": Tuning(32, 64, 32, kv_waves=2, mfma=16),
     "prefill_b4_h32": Tuning(32, 64, 1, kv_waves=2, mfma=16),
     "decode_b4_h16": Tuning(16, 64, 32, kv_waves=4, mfma=16),
     "prefill_b4_h16": Tuning(16, 64, 1, kv_waves=4, mfma=16),
-    "c1_decode_b1": Tuning(64, 64, 32, kv_waves=2),
-    "c2_decode_b8": Tuning(64, 64, 16, kv_waves=2),
+    "c1_decode_b1": Tuning(128, 32, 64, stages=4),
+    "c2_decode_b8": Tuning(32, 64, 8, kv_waves=2, mfma=16),
     "c3_decode_h16_mtp": Tuning(16, 64, 2, kv_waves=4, mfma=16),
     "c4_prefill_h16": Tuning(16, 64, 1, kv_waves=4, mfma=16),
-    "c5_prefill_h128": Tuning(64, 64, 1, kv_waves=2),
+    "c5_prefill_h128": Tuning(128, 32, 1, stages=4),
 }
 _BY_SHAPE = {}
 for _name, _shape in CASE_SHAPES.items():

@@ -30,8 +30,6 @@ int hip_fail(int err, const char* what) {
     return fail(err, "%s: %s (hipError_t %d)", what, hipGetErrorString((hipError_t)err), err);
 }
 
-constexpr int kTileRows = 64;
-constexpr int kStages = 2;
 
 int ceil_div(int a, int b) { return (a + b - 1) / b; }
 
@@ -39,6 +37,8 @@ int check_shape(int B, int SQ, int H, int L, int TOPK) {
     if (B <= 0 || SQ <= 0 || H <= 0 || L <= 0 || TOPK <= 0)
         return fail(-1, "all of B, SQ, H, L, TOPK must be positive (got %d, %d, %d, %d, %d)", B, SQ, H, L, TOPK);
     if (H % 16 != 0) return fail(-1, "H must be a multiple of 16 (got %d)", H);
+    // kv rows of one batch are addressed with 32-bit byte offsets
+    if (L >= (1 << 22)) return fail(-1, "L must be below 4194304 (got %d)", L);
     if ((int64_t)B * SQ > (int64_t)1 << 30) return fail(-1, "B*SQ too large");
     return 0;
 }
@@ -59,12 +59,12 @@ int dsa_plan_check(const dsa_plan* plan, int B, int SQ, int H, int L, int TOPK) 
     if (hpg <= 0 || hpg % mfma)
         return fail(-1, "heads_per_group must be a positive multiple of mfma=%d (got %d)", mfma, hpg);
     if (H % hpg) return fail(-1, "heads_per_group %d must divide H=%d", hpg, H);
-    if (bn != kTileRows) return fail(-1, "tile_rows must be %d (got %d)", kTileRows, bn);
-    if (plan->stages != kStages) return fail(-1, "stages must be %d (got %d)", kStages, plan->stages);
+    if (bn != 32 && bn != 64) return fail(-1, "tile_rows must be 32 or 64 (got %d)", bn);
     if (plan->kv_waves * (hpg / mfma) != 4)
         return fail(-1, "kv_waves * heads_per_group / mfma must be 4 (got kv_waves=%d)", plan->kv_waves);
     if (!dsa::fwd_variant_exists(hpg, plan->kv_waves, bn, plan->stages, mfma))
-        return fail(-1, "no kernel variant for heads_per_group=%d kv_waves=%d mfma=%d", hpg, plan->kv_waves, mfma);
+        return fail(-1, "no kernel variant for heads_per_group=%d kv_waves=%d tile_rows=%d stages=%d mfma=%d", hpg,
+                    plan->kv_waves, bn, plan->stages, mfma);
     const int ntiles = ceil_div(TOPK, bn);
     if (split < 1 || split > ntiles)
         return fail(-1, "split must be in [1, %d] for TOPK=%d (got %d)", ntiles, TOPK, split);
@@ -80,26 +80,27 @@ int dsa_plan_for(int B, int SQ, int H, int L, int TOPK, int num_cus, dsa_plan* o
     if (num_cus <= 0) return fail(-1, "num_cus must be positive (got %d)", num_cus);
     dsa_plan p{};
     // Four waves per workgroup.  Head counts that are multiples of 64 use the
-    // 32x32x16 MFMA variant (32 heads per wave, 64 heads x 2 row streams);
-    // other head counts use the 16x16x32 variant: 32 x 2 or 16 x 4.
+    // 32x32x16 MFMA variant (32 heads per wave): 128 heads x 1 row stream on
+    // 32-row tiles with a 4-stage ring, or 64 heads x 2 row streams on 64-row
+    // tiles; other head counts use the 16x16x32 variant: 32 x 2 or 16 x 4.
     const int64_t tokens = (int64_t)B * SQ;
-    if (H % 64 == 0) {
-        p.heads_per_group = 64, p.kv_waves = 2, p.mfma = 32;
+    if (H % 128 == 0) {
+        p.heads_per_group = 128, p.kv_waves = 1, p.mfma = 32, p.tile_rows = 32, p.stages = 4;
+    } else if (H % 64 == 0) {
+        p.heads_per_group = 64, p.kv_waves = 2, p.mfma = 32, p.tile_rows = 64, p.stages = 2;
     } else if (H % 32 == 0) {
-        p.heads_per_group = 32, p.kv_waves = 2, p.mfma = 16;
+        p.heads_per_group = 32, p.kv_waves = 2, p.mfma = 16, p.tile_rows = 64, p.stages = 2;
     } else {
-        p.heads_per_group = 16, p.kv_waves = 4, p.mfma = 16;
+        p.heads_per_group = 16, p.kv_waves = 4, p.mfma = 16, p.tile_rows = 64, p.stages = 2;
     }
-    p.tile_rows = kTileRows;
-    p.stages = kStages;
     // One 152 KiB workgroup fits a CU; split the KV range until the grid covers
     // every CU once, but never below one tile per split.
-    const int ntiles = ceil_div(TOPK, kTileRows);
+    const int ntiles = ceil_div(TOPK, p.tile_rows);
     const int64_t base = tokens * (H / p.heads_per_group);
     int split = 1;
     if (base < num_cus) split = (int)((num_cus + base - 1) / base);
     if (split > ntiles) split = ntiles;
-    const int min_split = ceil_div(ntiles * kTileRows, DSA_IDX_CAP);
+    const int min_split = ceil_div(ntiles * p.tile_rows, DSA_IDX_CAP);
     if (split < min_split) split = min_split;
     p.split = split;
     *out = p;

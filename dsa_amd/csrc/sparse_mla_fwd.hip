@@ -60,21 +60,11 @@ constexpr float kRescaleLog2 = 8.0f;
 constexpr float kRestartLog2 = 64.0f;
 
 // ------------------------------------------------------------ ring layout
-// 4 waves, 64-row tiles, 2 stages: [stage][64 rows][1024 B kv] then
-// [stage][64 rows][128 B rope], then the slot indices of the workgroup.
+// 4 waves per workgroup.  LDS: NSTAGE stages of [BN rows][1024 B kv] then
+// [BN rows][128 B rope], then the slot indices of the workgroup, then one
+// flag word (second-pass vote of the wide variant).
 constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
-constexpr int kBN = 64;
-constexpr int kKvBytes = kBN * 1024;
-constexpr int kRopeBytes = kBN * 128;
-constexpr int kStageBytes = kKvBytes + kRopeBytes;
-constexpr int kIdxOff = 2 * kStageBytes;
-constexpr int kGenOff = kIdxOff + DSA_IDX_CAP * 4;  // second-pass vote (wide variant)
-constexpr int kLdsBytes = kGenOff + 16;
-constexpr int kKvPerWave = kBN / kWaves;          // kv row gathers per wave per tile
-constexpr int kRopePerWave = kBN / 8 / kWaves;    // rope gathers (8 rows each)
-static_assert(kLdsBytes <= 160 * 1024, "LDS budget");
-
 // ---------------------------------------------------------------- LDS access
 template <typename T>
 __device__ __forceinline__ T lds_load(uint32_t addr) {
@@ -98,22 +88,58 @@ __device__ __forceinline__ void lds_barrier() {
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
-// s_waitcnt vmcnt(0), other counters untouched (gfx9 encoding).
-__device__ __forceinline__ void wait_vmcnt0() {
-    __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
+// s_waitcnt vmcnt(N), other counters untouched (gfx9 encoding).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-// Gather one 16-byte chunk per lane from global memory into LDS at
-// m0 + 16 * lane (the LDS base is wave-uniform by construction).  Issued as
-// inline asm so the compiler does not serialise later LDS reads behind it;
-// completion is tracked with wait_vmcnt0().
-__device__ __forceinline__ void gather16(uint32_t lds_wave_base, const void* gaddr) {
+typedef int rsrc_t __attribute__((ext_vector_type(4)));
+
+// Raw buffer resource over [base, base + bytes) (gfx9 descriptor: no stride,
+// 32-bit byte offsets).  All fields are wave-uniform.
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+    const uint64_t a = reinterpret_cast<uint64_t>(base);
+    rsrc_t r;
+    r[0] = __builtin_amdgcn_readfirstlane((int)(uint32_t)a);
+    r[1] = __builtin_amdgcn_readfirstlane((int)((a >> 32) & 0xffff));
+    r[2] = __builtin_amdgcn_readfirstlane((int)bytes);
+    r[3] = 0x00020000;
+    return r;
+}
+
+// Gathers write LDS with buffer_load_dwordx4 ... lds: lane l's 16 bytes land
+// at m0 + 16*l.  They are issued as inline asm so the compiler does not
+// serialise later LDS reads behind them; completion is tracked with
+// Ring::wait_tile().  m0 and the buffer offsets are wave-uniform by construction.
+//
+// One kv row: lane l loads bytes row_off + ((16*l) ^ xor16) of the buffer.
+// The XOR is part of the asm so no per-row lane offset is ever kept live.
+__device__ __forceinline__ void gather_row(uint32_t lds_base, rsrc_t rsrc, uint32_t row_off, uint32_t lane16,
+                                           uint32_t xor16) {
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
-    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off"
-                 :
-                 : "s"(__builtin_amdgcn_readfirstlane(lds_wave_base)), "v"(gaddr)
-                 : "memory", "m0");
+    uint32_t voff;
+    asm volatile(
+        "v_xor_b32 %0, %1, %2\n\t"
+        "s_mov_b32 m0, %3\n\t"
+        "buffer_load_dwordx4 %0, %4, %5 offen lds"
+        : "=&v"(voff)
+        : "s"(xor16), "v"(lane16), "s"(__builtin_amdgcn_readfirstlane(lds_base)), "s"(rsrc), "s"(row_off)
+        : "memory", "m0");
+#pragma clang diagnostic pop
+}
+// Arbitrary per-lane byte offsets (rope rows: 8 rows per instruction).
+__device__ __forceinline__ void gather_lanes(uint32_t lds_base, rsrc_t rsrc, uint32_t voff) {
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+    asm volatile(
+        "s_mov_b32 m0, %0\n\t"
+        "buffer_load_dwordx4 %1, %2, 0 offen lds"
+        :
+        : "s"(__builtin_amdgcn_readfirstlane(lds_base)), "v"(voff), "s"(rsrc)
+        : "memory", "m0");
 #pragma clang diagnostic pop
 }
 
@@ -125,13 +151,50 @@ __device__ __forceinline__ void gather16(uint32_t lds_wave_base, const void* gad
 // quarter-wave) and the transposed PV reads of both variants bank-conflict
 // free.  A rope row occupies 128 bytes (8 chunks): physical = c ^ sw_rope(r).
 __device__ __forceinline__ int sw_kv(int r) {
-    return ((r & 3) << 2) | (((r >> 2) & 1) << 1) | ((r >> 3) & 1);
+    return ((r & 3) << 2) | (((r >> 2) & 1) << 1) | ((r >> 3) & 1);  // uses r mod 16
 }
 __device__ __forceinline__ int sw_rope(int r) { return (r >> 1) & 7; }
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // ------------------------------------------------------------ shared pieces
+template <int BN_, int NSTAGE_>
+struct Ring {
+    static constexpr int BN = BN_;
+    static constexpr int NSTAGE = NSTAGE_;
+    static constexpr int KV_BYTES = BN * 1024;
+    static constexpr int STAGE_BYTES = BN * 1152;
+    static constexpr int IDX_OFF = NSTAGE * STAGE_BYTES;
+    static constexpr int FLAG_OFF = IDX_OFF + DSA_IDX_CAP * 4;
+    static constexpr int LDS_BYTES = FLAG_OFF + 16;
+    static constexpr int KV_PER_WAVE = BN / kWaves;        // kv row gathers per wave per tile
+    static constexpr int ROPE_PER_WAVE = BN / 8 / kWaves;  // rope gathers (8 rows each)
+    static constexpr int LOADS_PER_TILE = KV_PER_WAVE + ROPE_PER_WAVE;  // VMEM ops per wave
+    static_assert(BN % (8 * kWaves) == 0, "rope gathers split evenly over the waves");
+    static_assert(NSTAGE >= 2 && LOADS_PER_TILE * (NSTAGE - 2) < 64, "vmcnt range");
+    static_assert(LDS_BYTES <= 160 * 1024, "LDS budget");
+
+    __device__ static uint32_t stage(uint32_t lds, int t) { return lds + (uint32_t)(t % NSTAGE) * STAGE_BYTES; }
+
+    // Wait until this wave's gathers of tile t have landed, given that the
+    // tiles up to min(t + NSTAGE - 2, nt - 1) have been issued (in order).
+    __device__ static void wait_tile(int t, int nt) {
+        const int ahead = min(NSTAGE - 2, nt - 1 - t);
+        if constexpr (NSTAGE >= 4)
+            if (ahead >= 2) {
+                wait_vmcnt<2 * LOADS_PER_TILE>();
+                return;
+            }
+        if constexpr (NSTAGE >= 3)
+            if (ahead >= 1) {
+                wait_vmcnt<LOADS_PER_TILE>();
+                return;
+            }
+        wait_vmcnt<0>();
+    }
+    static_assert(NSTAGE <= 4, "wait_tile handles up to 4 stages");
+};
+
 struct WgCoords {
     int token, sp, hgi, b, nt, slot0;
 };
@@ -140,6 +203,7 @@ struct WgCoords {
 // are dispatched round-robin over the 8 XCDs; when possible all head groups
 // of one row group land on the same XCD so the gathered rows are fetched from
 // HBM once and re-read from that XCD's L2.
+template <int BN>
 __device__ __forceinline__ WgCoords wg_coords(const FwdParams& p) {
     const int wg = blockIdx.x;
     int rg, hgi;
@@ -159,47 +223,77 @@ __device__ __forceinline__ WgCoords wg_coords(const FwdParams& p) {
     const int t_begin = (int)(((int64_t)c.sp * p.ntiles) / p.nsplit);
     const int t_end = (int)(((int64_t)(c.sp + 1) * p.ntiles) / p.nsplit);
     c.nt = t_end - t_begin;
-    c.slot0 = t_begin * kBN;
+    c.slot0 = t_begin * BN;
     return c;
 }
 
-// Indices of the workgroup's slot range -> LDS, padded with -1 so a ragged
-// last tile is masked.  nslots <= DSA_IDX_CAP (checked on the host).
-__device__ __forceinline__ void load_indices(const FwdParams& p, const WgCoords& c, uint32_t idx_lds) {
+// Indices of the workgroup's slot range, padded with -1 so a ragged last
+// tile is masked (nslots <= DSA_IDX_CAP, checked on the host).  Split into a
+// global-load half and an LDS-store half so other loads can be issued in
+// between without waiting for these.
+struct IdxRegs {
+    int v[DSA_IDX_CAP / kThreads];
+};
+template <int BN>
+__device__ __forceinline__ IdxRegs fetch_indices(const FwdParams& p, const WgCoords& c) {
     const int32_t* gidx = p.idx + (int64_t)c.token * p.TOPK;
-    const int nslots = c.nt * kBN;
-    for (int s = threadIdx.x; s < nslots; s += kThreads) {
+    const int nslots = c.nt * BN;
+    IdxRegs r;
+#pragma unroll
+    for (int i = 0; i < DSA_IDX_CAP / kThreads; ++i) {
+        const int s = (int)threadIdx.x + i * kThreads;
         const int slot = c.slot0 + s;
-        lds_store<int>(idx_lds + 4 * s, slot < p.TOPK ? gidx[slot] : -1);
+        r.v[i] = (s < nslots && slot < p.TOPK) ? gidx[slot] : -1;
+    }
+    return r;
+}
+template <int BN>
+__device__ __forceinline__ void store_indices(const IdxRegs& r, const WgCoords& c, uint32_t idx_lds) {
+    const int nslots = c.nt * BN;
+#pragma unroll
+    for (int i = 0; i < DSA_IDX_CAP / kThreads; ++i) {
+        const int s = (int)threadIdx.x + i * kThreads;
+        if (s < nslots) lds_store<int>(idx_lds + 4 * s, r.v[i]);
     }
 }
 
+// Buffer resources over this workgroup's batch of kv and k_rope.
+struct Gather {
+    rsrc_t kv, kr;
+};
+__device__ __forceinline__ Gather make_gather(const FwdParams& p, int b) {
+    const int64_t rows = (int64_t)b * p.L;
+    Gather g;
+    g.kv = make_rsrc(reinterpret_cast<const char*>(p.kv) + rows * 1024, (uint32_t)p.L * 1024u);
+    g.kr = make_rsrc(reinterpret_cast<const char*>(p.k_rope) + rows * 128, (uint32_t)p.L * 128u);
+    return g;
+}
+
 // Gather of workgroup tile t into ring stage `stage` (LDS byte address).
-// Wave w fetches kv rows [16w, 16w+16) (1 KiB each, one instruction per row)
-// and rope rows [16w, 16w+16) (8 rows per instruction).
-__device__ __forceinline__ void issue_tile(const FwdParams& p, int t, uint32_t stage, uint32_t idx_lds,
-                                           int64_t kv_batch, int wave, int lane) {
-    const char* kv_base = reinterpret_cast<const char*>(p.kv);
-    const char* kr_base = reinterpret_cast<const char*>(p.k_rope);
+// Wave w fetches kv rows [w*KV_PER_WAVE, (w+1)*KV_PER_WAVE) (1 KiB each, one
+// instruction per row) and ROPE_PER_WAVE groups of 8 rope rows.  Row indices
+// are clamped to [0, L) for the address; the mask uses the raw index.
+template <class R>
+__device__ __forceinline__ void issue_tile(const FwdParams& p, const Gather& gt, int t, uint32_t stage,
+                                           uint32_t idx_lds, int wave, int lane) {
     const int L = p.L;
-    const int r0 = wave * kKvPerWave;
-    const int my_id = lds_load<int>(idx_lds + 4 * (t * kBN + r0 + (lane % kKvPerWave)));
+    const int r0 = wave * R::KV_PER_WAVE;
+    const int my_id = lds_load<int>(idx_lds + 4 * (t * R::BN + r0 + (lane % R::KV_PER_WAVE)));
+    const uint32_t my_off = (uint32_t)min(max(my_id, 0), L - 1) << 10;
+    const uint32_t lane16 = (uint32_t)lane << 4;
 #pragma unroll
-    for (int rr = 0; rr < kKvPerWave; ++rr) {
+    for (int rr = 0; rr < R::KV_PER_WAVE; ++rr) {
         const int r = r0 + rr;
-        int id = __builtin_amdgcn_readlane(my_id, rr);
-        id = min(max(id, 0), L - 1);  // address clamp; the mask uses the raw index
-        const char* src = kv_base + ((kv_batch + id) << 10) + ((lane ^ sw_kv(r)) << 4);
-        gather16(stage + r * 1024, src);
+        const uint32_t row_off = __builtin_amdgcn_readlane(my_off, rr);
+        gather_row(stage + r * 1024, gt.kv, row_off, lane16, (uint32_t)sw_kv(r) << 4);
     }
 #pragma unroll
-    for (int jj = 0; jj < kRopePerWave; ++jj) {
-        const int j = wave * kRopePerWave + jj;
+    for (int jj = 0; jj < R::ROPE_PER_WAVE; ++jj) {
+        const int j = wave * R::ROPE_PER_WAVE + jj;
         const int r = j * 8 + (lane >> 3);
-        int id = lds_load<int>(idx_lds + 4 * (t * kBN + r));
-        id = min(max(id, 0), L - 1);
-        const char* src = kr_base + ((kv_batch + id) << 7) + (((lane & 7) ^ sw_rope(r)) << 4);
-        gather16(stage + kKvBytes + j * 1024, src);
+        const int id = lds_load<int>(idx_lds + 4 * (t * R::BN + r));
+        const uint32_t voff = ((uint32_t)min(max(id, 0), L - 1) << 7) + (((lane & 7) ^ sw_rope(r)) << 4);
+        gather_lanes(stage + R::KV_BYTES + j * 1024, gt.kr, voff);
     }
 }
 
@@ -214,17 +308,17 @@ __device__ __forceinline__ void store_bf16x4(uint16_t* dst, float a, float b, fl
 }
 
 // ====================================================================== wide
-// HW head-waves of 32 heads x KW kv-waves (HW * KW == 4).  Wave (hw, kw)
-// processes rows [kw*RPW, (kw+1)*RPW) of every tile for heads hw*32..+31.
+// HW head-waves of 32 heads x KW kv-waves (HW * KW == 4); every wave processes
+// one 32-row subtile of each BN-row tile (BN == 32 * KW): wave (hw, kw) owns
+// rows [32*kw, 32*kw + 32) for heads hw*32..+31.
 //
 // 32x32x16 operand layouts (lane i, h = i >> 5, n = i & 31):
 //   A[m = n][k = 8h + j], B[k = 8h + j][n = n], C[m = 8*(r>>2) + 4h + (r&3)][n = n].
-template <int HW, int KW>
+template <int HW, int KW, int BN, int NSTAGE>
 __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd_wide(FwdParams p) {
-    static_assert(HW * KW == kWaves && (KW == 1 || KW == 2), "wide variant shape");
-    constexpr int RPW = kBN / KW;   // rows per wave per tile
-    constexpr int NSUB = RPW / 32;  // 32-row subtiles per wave per tile
-    __shared__ __attribute__((aligned(1024))) char smem[kLdsBytes];
+    using R = Ring<BN, NSTAGE>;
+    static_assert(HW * KW == kWaves && BN == 32 * KW, "wide variant shape");
+    __shared__ __attribute__((aligned(1024))) char smem[R::LDS_BYTES];
     const uint32_t lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)smem;
 
     const int lane = threadIdx.x & 63;
@@ -236,9 +330,14 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd_wide(FwdParams p) 
     const int G = lane >> 4;
     const int n16 = lane & 15;
 
-    const WgCoords c = wg_coords(p);
+    const WgCoords c = wg_coords<BN>(p);
     const int head = c.hgi * (32 * HW) + hw * 32 + n32;  // this lane's head
     const int L = p.L;
+    const uint32_t idx_lds = lds + R::IDX_OFF;
+
+    // Index loads first: the first gather depends on them, Q only on the
+    // first MFMA.
+    const IdxRegs ids = fetch_indices<BN>(p, c);
 
     // ---- Q fragments: B operand of S^T = K . Q^T.  Lane holds
     // Q[head][16*ks + 8*h .. +7]; ks 32..35 come from q_rope.
@@ -251,28 +350,25 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd_wide(FwdParams p) 
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) qf[32 + ks] = *reinterpret_cast<const bf16x8*>(rrow + 16 * ks);
     }
-
-    const uint32_t idx_lds = lds + kIdxOff;
-    load_indices(p, c, idx_lds);
+    store_indices<BN>(ids, c, idx_lds);
     lds_barrier();
-    const int64_t kv_batch = (int64_t)c.b * L;
+    const Gather gt = make_gather(p, c.b);
 
     // ---- per-lane LDS offsets.  Swizzles depend on the row mod 16 and XOR
     // only the low 4 bits of a chunk index, so every fragment address is a
     // per-lane base plus a compile-time multiple of 256 bytes.
-    const int rowbase = kw * RPW;
-    // QK A operand: row rowbase + 32*s + n32, logical chunk 2*ks + h =
-    // 16*(ks >> 3) + (2*(ks & 7) + h).
+    const int row0 = kw * 32;
+    // QK A operand: row row0 + n32, logical chunk 2*ks + h = 16*(ks >> 3) + (2*(ks & 7) + h).
     uint32_t qk_off[8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) qk_off[j] = ((2 * j + h) ^ sw_kv(n32 & 15)) << 4;
+    for (int j = 0; j < 8; ++j) qk_off[j] = ((2 * j + h) ^ sw_kv(n32)) << 4;
     uint32_t rp_off[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) rp_off[j] = ((2 * j + h) ^ sw_rope(n32 & 15)) << 4;
     // PV A operand (transposed reads): for k-step kk and read rd, row
-    // rowbase + 32*s + 16*kk + 8*rd + 4*h + n16/4, columns 32*cb + 16*(G&1) +
-    // 4*(n16&3) -> logical chunk 4*cb + 2*(G&1) + ((n16&3)>>1) =
-    // 16*(cb >> 2) + (4*(cb&3) + ...), byte 8*(n16&1) within the chunk.
+    // row0 + 16*kk + 8*rd + 4*h + n16/4, columns 32*cb + 16*(G&1) + 4*(n16&3)
+    // -> logical chunk 4*cb + 2*(G&1) + ((n16&3)>>1) = 16*(cb >> 2) + (4*(cb&3) + ...),
+    // byte 8*(n16&1) within the chunk.
     const int tr_row = 4 * h + (n16 >> 2);
     uint32_t tr_off[2][4];
 #pragma unroll
@@ -287,7 +383,7 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd_wide(FwdParams p) 
     float m_ref = -FLT_MAX;   // reference max of P
     float m_true = -FLT_MAX;  // exact running max
     float l_run = 0.f;        // per-lane partial of the head's sum, relative to m_ref
-    const uint32_t flag_lds = lds + kGenOff;
+    const uint32_t flag_lds = lds + R::FLAG_OFF;
 
     // At most two passes over the range (see kRestartLog2).  Pass 0 fixes
     // m_ref at the first tile with a valid row; if any head's max later grows
@@ -300,91 +396,100 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd_wide(FwdParams p) 
         l_run = 0.f;
         if (pass == 1) m_ref = m_true;
         bool overflow = false;
-        if (c.nt > 0) issue_tile(p, 0, lds, idx_lds, kv_batch, wave, lane);
+#pragma unroll
+        for (int i = 0; i < NSTAGE - 1; ++i)
+            if (i < c.nt) issue_tile<R>(p, gt, i, R::stage(lds, i), idx_lds, wave, lane);
 
         for (int t = 0; t < c.nt; ++t) {
-            const int st = t & 1;
-            wait_vmcnt0();
-            lds_barrier();
-            if (t + 1 < c.nt) issue_tile(p, t + 1, lds + (st ^ 1) * kStageBytes, idx_lds, kv_batch, wave, lane);
-            const uint32_t stage = lds + st * kStageBytes;
+            R::wait_tile(t, c.nt);
+            lds_barrier();  // tile t visible to all waves; stage of tile t-1 free
+            if (t + NSTAGE - 1 < c.nt)
+                issue_tile<R>(p, gt, t + NSTAGE - 1, R::stage(lds, t + NSTAGE - 1), idx_lds, wave, lane);
+            const uint32_t stage = R::stage(lds, t);
 
+            // ---- S^T = K . Q^T for rows row0..row0+31: two independent MFMA
+            // chains (even / odd k-steps) in an explicit 4-deep LDS pipeline;
+            // the scheduler is fenced per step so at most 4 fragments are live.
+            f32x16 sacc0 = f32x16{}, sacc1 = f32x16{};
+            const uint32_t rowa = stage + (row0 + n32) * 1024;
+            const uint32_t rowr = stage + R::KV_BYTES + (row0 + n32) * 128;
+            uint32_t qa[8], ra[4];
 #pragma unroll
-            for (int s = 0; s < NSUB; ++s) {
+            for (int j = 0; j < 8; ++j) qa[j] = rowa + qk_off[j];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) ra[j] = rowr + rp_off[j];
+            auto kfrag = [&](int ks) -> bf16x8 {
+                return ks < 32 ? lds_load<bf16x8>(qa[ks & 7] + ((ks >> 3) << 8)) : lds_load<bf16x8>(ra[ks - 32]);
+            };
+            bf16x8 kf[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) kf[j] = kfrag(j);
+#pragma unroll
+            for (int ks = 0; ks < 36; ++ks) {
+                if (ks & 1)
+                    sacc1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[ks & 3], qf[ks], sacc1, 0, 0, 0);
+                else
+                    sacc0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[ks & 3], qf[ks], sacc0, 0, 0, 0);
+                if (ks + 4 < 36) kf[ks & 3] = kfrag(ks + 4);
                 __builtin_amdgcn_sched_barrier(0);
-                const int row0 = rowbase + 32 * s;
-                // ---- S^T = K . Q^T for rows row0..row0+31.  Explicit 4-deep
-                // software pipeline: fragment ks+4 is read while MFMA ks runs,
-                // and the scheduler is fenced per step so at most 4 fragments
-                // are live.
-                f32x16 sacc = f32x16{};
-                const uint32_t rowa = stage + (row0 + n32) * 1024;
-                const uint32_t rowr = stage + kKvBytes + (row0 + n32) * 128;
-                auto kfrag = [&](int ks) -> bf16x8 {
-                    return ks < 32 ? lds_load<bf16x8>(rowa + qk_off[ks & 7] + ((ks >> 3) << 8))
-                                   : lds_load<bf16x8>(rowr + rp_off[ks - 32]);
-                };
-                bf16x8 kf[4];
-#pragma unroll
-                for (int j = 0; j < 4; ++j) kf[j] = kfrag(j);
-#pragma unroll
-                for (int ks = 0; ks < 36; ++ks) {
-                    sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[ks & 3], qf[ks], sacc, 0, 0, 0);
-                    if (ks + 4 < 36) kf[ks & 3] = kfrag(ks + 4);
-                    __builtin_amdgcn_sched_barrier(0);
-                }
+            }
 
-                // ---- scale, mask, online softmax.  Lane holds rows
-                // row0 + 8*q + 4*h + (0..3) for q = 0..3 (register 4q + j) of head n32.
-                float x[16];
-                float mloc = -INFINITY;
+            // ---- scale, mask, online softmax.  Lane holds rows
+            // row0 + 8*q + 4*h + (0..3) for q = 0..3 (register 4q + j) of head n32.
+            float x[16];
+            float mloc = -INFINITY;
 #pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const i32x4 iv = lds_load<i32x4>(idx_lds + 4 * (t * kBN + row0 + 8 * q + 4 * h));
+            for (int q = 0; q < 4; ++q) {
+                const i32x4 iv = lds_load<i32x4>(idx_lds + 4 * (t * BN + row0 + 8 * q + 4 * h));
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        const bool valid = (unsigned)iv[j] < (unsigned)L;
-                        const float v = valid ? sacc[4 * q + j] * kScoreLog2 : -INFINITY;
-                        x[4 * q + j] = v;
-                        mloc = fmaxf(mloc, v);
-                    }
+                for (int j = 0; j < 4; ++j) {
+                    const bool valid = (unsigned)iv[j] < (unsigned)L;
+                    const float sv = sacc0[4 * q + j] + sacc1[4 * q + j];
+                    const float v = valid ? sv * kScoreLog2 : -INFINITY;
+                    x[4 * q + j] = v;
+                    mloc = fmaxf(mloc, v);
                 }
-                mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
-                m_true = fmaxf(m_true, mloc);
-                if (m_ref == -FLT_MAX) m_ref = m_true;  // first valid rows: O and l are still zero
-                overflow |= m_true > m_ref + kRestartLog2;
-                // P <= 2^kRestartLog2 unless this pass is to be discarded; the
-                // clamp keeps a discarded pass free of inf.
-                bf16x8 pk[2];
-                float psum = 0.f;
+            }
+            mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
+            m_true = fmaxf(m_true, mloc);
+            if (m_ref == -FLT_MAX) m_ref = m_true;  // first valid rows: O and l are still zero
+            overflow |= m_true > m_ref + kRestartLog2;
+            // P <= 2^kRestartLog2 unless this pass is to be discarded; the
+            // clamp keeps a discarded pass free of inf.
+            bf16x8 pk[2];
+            float psum = 0.f;
 #pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const float e = fast_exp2(fminf(x[r] - m_ref, kRestartLog2));
-                    psum += e;
-                    pk[r >> 3][r & 7] = (__bf16)e;
-                }
-                l_run += psum;
+            for (int r = 0; r < 16; ++r) {
+                const float e = fast_exp2(fminf(x[r] - m_ref, kRestartLog2));
+                psum += e;
+                pk[r >> 3][r & 7] = (__bf16)e;
+            }
+            l_run += psum;
 
-                // ---- O^T += V^T . P^T, two k-steps of 16 rows x 16 column
-                // blocks, same 4-deep pipeline over the 32 (kk, cb) steps.
-                const uint32_t vrow = stage + (row0 + tr_row) * 1024;
-                auto vfrag = [&](int step) -> bf16x8 {
-                    const int kk = step >> 4, cb = step & 15;
-                    const uint32_t r0a = vrow + kk * 16 * 1024 + ((cb >> 2) << 8);
-                    const bf16x4 v0 = lds_load_tr(r0a + tr_off[0][cb & 3]);
-                    const bf16x4 v1 = lds_load_tr(r0a + 8 * 1024 + tr_off[1][cb & 3]);
-                    return __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7);
-                };
-                bf16x8 vf[4];
+            // ---- O^T += V^T . P^T, two k-steps of 16 rows x 16 column blocks,
+            // same 4-deep pipeline over the 32 (kk, cb) steps.
+            const uint32_t vrow = stage + (row0 + tr_row) * 1024;
+            uint32_t va[2][4];
 #pragma unroll
-                for (int j = 0; j < 4; ++j) vf[j] = vfrag(j);
+            for (int rd = 0; rd < 2; ++rd)
 #pragma unroll
-                for (int step = 0; step < 32; ++step) {
-                    const int kk = step >> 4, cb = step & 15;
-                    oacc[cb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[step & 3], pk[kk], oacc[cb], 0, 0, 0);
-                    if (step + 4 < 32) vf[step & 3] = vfrag(step + 4);
-                    __builtin_amdgcn_sched_barrier(0);
-                }
+                for (int j = 0; j < 4; ++j) va[rd][j] = vrow + rd * 8 * 1024 + tr_off[rd][j];
+            auto vfrag = [&](int step) -> bf16x8 {
+                const int kk = step >> 4, cb = step & 15;
+                const uint32_t imm = kk * 16 * 1024 + ((cb >> 2) << 8);
+                const bf16x4 v0 = lds_load_tr(va[0][cb & 3] + imm);
+                const bf16x4 v1 = lds_load_tr(va[1][cb & 3] + imm);
+                return __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7);
+            };
+            bf16x8 vf[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) vf[j] = vfrag(j);
+#pragma unroll
+            for (int step = 0; step < 32; ++step) {
+                const int kk = step >> 4, cb = step & 15;
+                oacc[cb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[step & 3], pk[kk], oacc[cb], 0, 0, 0);
+                if (step + 4 < 32) vf[step & 3] = vfrag(step + 4);
+                __builtin_amdgcn_sched_barrier(0);
             }
         }
         // ---- workgroup vote: does any head need pass 1?
@@ -402,9 +507,9 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd_wide(FwdParams p) 
         // kv-wave 1 hands (m_ref, m_true, l, O) to kv-wave 0 of the same head
         // slice through LDS; kv-wave 0 merges (m = max, w = exp(m_k - m)).
         constexpr int OX_STRIDE = 516;  // floats per head row, padded
-        static_assert(2 * 32 * OX_STRIDE * 4 <= kIdxOff, "exchange fits the ring");
+        static_assert(HW * 32 * OX_STRIDE * 4 <= R::IDX_OFF, "exchange fits the ring");
         lds_barrier();                  // every wave is past its last ring read
-        const uint32_t ml = lds + kIdxOff;
+        const uint32_t ml = lds + R::IDX_OFF;
         const uint32_t ox = lds + ((hw * 32 + n32) * OX_STRIDE + 4 * h) * 4;
         if (kw == 1) {
             if (h == 0) {
@@ -482,10 +587,12 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd_wide(FwdParams p) 
 template <int HW, int KW>
 __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd_narrow(FwdParams p) {
     static_assert(HW * KW == kWaves, "narrow variant shape");
+    using R = Ring<64, 2>;
+    constexpr int kBN = R::BN;
     constexpr int RPW = kBN / KW;   // tile rows per wave
     constexpr int NSUB = RPW / 16;  // 16-row subtiles per wave
     static_assert(RPW == 16 || RPW == 32 || RPW == 64, "rows per wave");
-    __shared__ __attribute__((aligned(1024))) char smem[kLdsBytes];
+    __shared__ __attribute__((aligned(1024))) char smem[R::LDS_BYTES];
     const uint32_t lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)smem;
 
     const int lane = threadIdx.x & 63;
@@ -495,7 +602,7 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd_narrow(FwdParams p
     const int g = lane >> 4;
     const int n16 = lane & 15;
 
-    const WgCoords c = wg_coords(p);
+    const WgCoords c = wg_coords<kBN>(p);
     const int head = c.hgi * (16 * HW) + hw * 16 + n16;  // this lane's head
     const int L = p.L;
 
@@ -510,10 +617,10 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd_narrow(FwdParams p
         qf[17] = *reinterpret_cast<const bf16x8*>(rrow + 32);
     }
 
-    const uint32_t idx_lds = lds + kIdxOff;
-    load_indices(p, c, idx_lds);
+    const uint32_t idx_lds = lds + R::IDX_OFF;
+    store_indices<kBN>(fetch_indices<kBN>(p, c), c, idx_lds);
     lds_barrier();
-    const int64_t kv_batch = (int64_t)c.b * L;
+    const Gather gt = make_gather(p, c.b);
 
     // ---- per-lane LDS offsets (see the wide variant).
     const int rowbase = kw * RPW;
@@ -540,15 +647,14 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd_narrow(FwdParams p
     float m_true = -FLT_MAX;
     float l_run = 0.f;
 
-    if (c.nt > 0) issue_tile(p, 0, lds, idx_lds, kv_batch, wave, lane);
+    if (c.nt > 0) issue_tile<R>(p, gt, 0, R::stage(lds, 0), idx_lds, wave, lane);
 
     for (int t = 0; t < c.nt; ++t) {
-        const int st = t & 1;
-        wait_vmcnt0();
+        R::wait_tile(t, c.nt);
         lds_barrier();
-        if (t + 1 < c.nt) issue_tile(p, t + 1, lds + (st ^ 1) * kStageBytes, idx_lds, kv_batch, wave, lane);
+        if (t + 1 < c.nt) issue_tile<R>(p, gt, t + 1, R::stage(lds, t + 1), idx_lds, wave, lane);
 
-        const uint32_t stage = lds + st * kStageBytes;
+        const uint32_t stage = R::stage(lds, t);
         // ---- S^T = K . Q^T for this wave's rows
         f32x4 sacc[NSUB];
 #pragma unroll
@@ -560,7 +666,7 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd_narrow(FwdParams p
                 const bf16x8 a = lds_load<bf16x8>(rowa + qk_off[ks & 3] + ((ks >> 2) << 8));
                 sacc[s] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qf[ks], sacc[s], 0, 0, 0);
             }
-            const uint32_t rowr = stage + kKvBytes + (rowbase + 16 * s + n16) * 128;
+            const uint32_t rowr = stage + R::KV_BYTES + (rowbase + 16 * s + n16) * 128;
 #pragma unroll
             for (int ks = 0; ks < 2; ++ks) {
                 const bf16x8 a = lds_load<bf16x8>(rowr + rp_off[ks]);
@@ -649,9 +755,9 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd_narrow(FwdParams p
         // Merge the KW row-split waves of each head slice through LDS (same
         // FP32 merge as the split merge): M = max m_ref_k, w_k = exp(m_ref_k - M).
         constexpr int OX_STRIDE = 516;  // floats per head row (padded)
-        static_assert(kWaves * 16 * OX_STRIDE * 4 <= kIdxOff, "exchange fits the ring");
+        static_assert(kWaves * 16 * OX_STRIDE * 4 <= R::IDX_OFF, "exchange fits the ring");
         lds_barrier();  // every wave is past its last ring read
-        const uint32_t ml = lds + kIdxOff;  // [3][4 waves][16] floats: m_ref, m_true, l
+        const uint32_t ml = lds + R::IDX_OFF;  // [3][4 waves][16] floats: m_ref, m_true, l
         if (g == 0) {
             lds_store<float>(ml + 4 * (wave * 16 + n16), m_ref);
             lds_store<float>(ml + 4 * (kWaves * 16 + wave * 16 + n16), m_true);
@@ -737,9 +843,10 @@ int launch(K kernel, const FwdParams& p, hipStream_t stream) {
 }  // namespace
 
 bool fwd_variant_exists(int hpg, int kvw, int bn, int stages, int mfma) {
-    if (bn != kBN || stages != 2) return false;
-    if (mfma == 32) return hpg == 64 && kvw == 2;
-    if (mfma == 16) return (hpg == 64 && kvw == 1) || (hpg == 32 && kvw == 2) || (hpg == 16 && kvw == 4);
+    if (mfma == 32)
+        return (hpg == 128 && kvw == 1 && bn == 32 && stages == 4) || (hpg == 64 && kvw == 2 && bn == 64 && stages == 2);
+    if (mfma == 16 && bn == 64 && stages == 2)
+        return (hpg == 64 && kvw == 1) || (hpg == 32 && kvw == 2) || (hpg == 16 && kvw == 4);
     return false;
 }
 
@@ -747,7 +854,10 @@ int64_t fwd_grid(const FwdParams& p) { return (int64_t)p.rowgroups * p.hgroups; 
 
 int launch_fwd(const FwdParams& p, int hpg, int kvw, int bn, int stages, int mfma, hipStream_t stream) {
     if (!fwd_variant_exists(hpg, kvw, bn, stages, mfma)) return (int)hipErrorInvalidValue;
-    if (mfma == 32) return launch(sparse_mla_fwd_wide<2, 2>, p, stream);
+    if (mfma == 32) {
+        if (hpg == 128) return launch(sparse_mla_fwd_wide<4, 1, 32, 4>, p, stream);
+        return launch(sparse_mla_fwd_wide<2, 2, 64, 2>, p, stream);
+    }
     if (hpg == 64) return launch(sparse_mla_fwd_narrow<4, 1>, p, stream);
     if (hpg == 32) return launch(sparse_mla_fwd_narrow<2, 2>, p, stream);
     return launch(sparse_mla_fwd_narrow<1, 4>, p, stream);

@@ -48,14 +48,15 @@ extern "C" {
  * fields were Ascend-specific (BM, BN, split, direct_nz, pv_cols, share_score).
  *
  *   heads_per_group : query heads one workgroup owns; divides H
- *   tile_rows       : gathered rows per LDS ring stage (64)
+ *   tile_rows       : gathered rows per LDS ring stage (32 or 64)
  *   split           : KV splits per (token, head group); > 1 adds the FP32 merge
  *   kv_waves        : waves that share a head slice and split each tile's rows
  *                     (heads_per_group / mfma * kv_waves == 4)
- *   stages          : LDS ring depth (2)
+ *   stages          : LDS ring depth (2 or 4)
  *   mfma            : heads per wave = MFMA block: 32 (v_mfma_f32_32x32x16_bf16;
- *                     heads_per_group 64, kv_waves 2) or 16 (v_mfma_f32_16x16x32_bf16;
- *                     heads_per_group 64, 32 or 16)
+ *                     heads_per_group 128 with tile_rows 32 and 4 stages, or 64
+ *                     with kv_waves 2) or 16 (v_mfma_f32_16x16x32_bf16;
+ *                     heads_per_group 64, 32 or 16; tile_rows 64, 2 stages)
  */
 typedef struct dsa_plan {
     int32_t heads_per_group;

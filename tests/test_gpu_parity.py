@@ -114,7 +114,8 @@ def test_c5_sampled_tokens_per_family():
 
 
 # ------------------------------------------------------- plans, edges, invariants
-PLANS_H128 = [Tuning(64, 64, 1, kv_waves=2), Tuning(64, 64, 2, kv_waves=2), Tuning(64, 64, 7, kv_waves=2),
+PLANS_H128 = [Tuning(128, 32, 1, stages=4), Tuning(128, 32, 3, stages=4), Tuning(128, 32, 64, stages=4),
+              Tuning(64, 64, 1, kv_waves=2), Tuning(64, 64, 2, kv_waves=2), Tuning(64, 64, 7, kv_waves=2),
               Tuning(64, 64, 32, kv_waves=2),
               Tuning(64, 64, 1, mfma=16), Tuning(64, 64, 32, mfma=16),
               Tuning(32, 64, 1, kv_waves=2, mfma=16), Tuning(32, 64, 5, kv_waves=2, mfma=16),

@@ -116,6 +116,7 @@ TUNING_MUTATIONS = {
     "bm not dividing H": Tuning(64, 64, 1, kv_waves=2),
     "bm 48": Tuning(48, 64, 1, mfma=16),
     "bn 128": Tuning(16, 128, 1, kv_waves=4, mfma=16),
+    "narrow bn 32": Tuning(16, 32, 1, kv_waves=4, mfma=16),
     "split 0": Tuning(16, 64, 0, kv_waves=4, mfma=16),
     "split > tiles": Tuning(16, 64, 2, kv_waves=4, mfma=16),
     "kv_waves mismatch": Tuning(16, 64, 1, kv_waves=1, mfma=16),
