@@ -49,14 +49,13 @@ typedef __attribute__((__vector_size__(4 * sizeof(int)))) int i32x4;
 // log2 units, so exp(score - max) == exp2(x - x_max).
 constexpr float kScoreLog2 = (float)(1.4426950408889634 / 24.0);
 constexpr float kLn2 = 0.69314718055994531f;
-// Narrow variant: P is formed against a reference max m_ref that only moves
-// when the true running max exceeds it by more than this (log2 units); then
-// O and l are rescaled.  P <= 2^8, so bf16 P keeps its relative precision.
-constexpr float kRescaleLog2 = 8.0f;
-// Wide variant: m_ref is fixed at the first tile with a valid row and P <=
-// 2^kRestartLog2; a head whose running max exceeds m_ref by more than that
-// makes the workgroup recompute its range once with m_ref = the exact max.
-// This keeps the 256 O accumulators out of VALU work inside the loop.
+// P is formed against a reference max m_ref fixed at the first tile with a
+// valid row and is clamped at 2^kRestartLog2; a head whose running max exceeds
+// m_ref by more than that makes the workgroup recompute its range once with
+// m_ref = the exact max.  The O accumulators therefore never see VALU work
+// inside the tile loop (a rescale there would move every accumulator between
+// AGPRs and VGPRs on every tile).  bf16 P keeps its relative precision at any
+// scale and FP32 O, l stay far from overflow (2^64 * TOPK).
 constexpr float kRestartLog2 = 64.0f;
 
 // ------------------------------------------------------------ ring layout
@@ -236,25 +235,29 @@ struct IdxRegs {
 };
 template <int BN>
 __device__ __forceinline__ IdxRegs fetch_indices(const FwdParams& p, const WgCoords& c) {
-    const int32_t* gidx = p.idx + (int64_t)c.token * p.TOPK;
+    // Buffer loads over the token's index row: a slot past TOPK reads 0
+    // (hardware range check) and is then masked to -1.  Being intrinsics
+    // rather than plain loads, they are never turned into branches around
+    // each load, so all of them issue back to back.
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<int32_t*>(p.idx + (int64_t)c.token * p.TOPK), (short)0, p.TOPK * 4, 0x00020000);
     const int nslots = c.nt * BN;
     IdxRegs r;
 #pragma unroll
     for (int i = 0; i < DSA_IDX_CAP / kThreads; ++i) {
         const int s = (int)threadIdx.x + i * kThreads;
-        const int slot = c.slot0 + s;
-        r.v[i] = (s < nslots && slot < p.TOPK) ? gidx[slot] : -1;
+        const int v = __builtin_amdgcn_raw_buffer_load_b32(rs, (c.slot0 + s) * 4, 0, 0);
+        r.v[i] = ((s < nslots) & (c.slot0 + s < p.TOPK)) ? v : -1;
     }
     return r;
 }
-template <int BN>
-__device__ __forceinline__ void store_indices(const IdxRegs& r, const WgCoords& c, uint32_t idx_lds) {
-    const int nslots = c.nt * BN;
+// Every entry of the cache is written (slots past the range hold -1): a
+// conditional store would let the compiler sink each global load into its
+// branch and wait for it there, serialising the loads.
+__device__ __forceinline__ void store_indices(const IdxRegs& r, uint32_t idx_lds) {
 #pragma unroll
-    for (int i = 0; i < DSA_IDX_CAP / kThreads; ++i) {
-        const int s = (int)threadIdx.x + i * kThreads;
-        if (s < nslots) lds_store<int>(idx_lds + 4 * s, r.v[i]);
-    }
+    for (int i = 0; i < DSA_IDX_CAP / kThreads; ++i)
+        lds_store<int>(idx_lds + 4 * ((int)threadIdx.x + i * kThreads), r.v[i]);
 }
 
 // Buffer resources over this workgroup's batch of kv and k_rope.
@@ -327,8 +330,6 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd_wide(FwdParams p) 
     const int kw = wave / HW;
     const int h = lane >> 5;
     const int n32 = lane & 31;
-    const int G = lane >> 4;
-    const int n16 = lane & 15;
 
     const WgCoords c = wg_coords<BN>(p);
     const int head = c.hgi * (32 * HW) + hw * 32 + n32;  // this lane's head
@@ -350,33 +351,11 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd_wide(FwdParams p) 
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) qf[32 + ks] = *reinterpret_cast<const bf16x8*>(rrow + 16 * ks);
     }
-    store_indices<BN>(ids, c, idx_lds);
+    store_indices(ids, idx_lds);
     lds_barrier();
     const Gather gt = make_gather(p, c.b);
 
-    // ---- per-lane LDS offsets.  Swizzles depend on the row mod 16 and XOR
-    // only the low 4 bits of a chunk index, so every fragment address is a
-    // per-lane base plus a compile-time multiple of 256 bytes.
     const int row0 = kw * 32;
-    // QK A operand: row row0 + n32, logical chunk 2*ks + h = 16*(ks >> 3) + (2*(ks & 7) + h).
-    uint32_t qk_off[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) qk_off[j] = ((2 * j + h) ^ sw_kv(n32)) << 4;
-    uint32_t rp_off[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) rp_off[j] = ((2 * j + h) ^ sw_rope(n32 & 15)) << 4;
-    // PV A operand (transposed reads): for k-step kk and read rd, row
-    // row0 + 16*kk + 8*rd + 4*h + n16/4, columns 32*cb + 16*(G&1) + 4*(n16&3)
-    // -> logical chunk 4*cb + 2*(G&1) + ((n16&3)>>1) = 16*(cb >> 2) + (4*(cb&3) + ...),
-    // byte 8*(n16&1) within the chunk.
-    const int tr_row = 4 * h + (n16 >> 2);
-    uint32_t tr_off[2][4];
-#pragma unroll
-    for (int rd = 0; rd < 2; ++rd)
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-            tr_off[rd][j] = (((4 * j + 2 * (G & 1) + ((n16 & 3) >> 1)) ^ sw_kv(tr_row + 8 * rd)) << 4) +
-                            ((n16 & 1) << 3);
 
     // ---- running state (log2 units)
     f32x16 oacc[16];
@@ -399,6 +378,10 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd_wide(FwdParams p) 
 #pragma unroll
         for (int i = 0; i < NSTAGE - 1; ++i)
             if (i < c.nt) issue_tile<R>(p, gt, i, R::stage(lds, i), idx_lds, wave, lane);
+        // The Q loads complete here, with the first tiles.  The compiler does
+        // not count the gathers (inline asm), so a wait it placed for Q inside
+        // the loop would be a vmcnt(0) on every tile, draining the ring.
+        wait_vmcnt<0>();
 
         for (int t = 0; t < c.nt; ++t) {
             R::wait_tile(t, c.nt);
@@ -406,18 +389,29 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd_wide(FwdParams p) 
             if (t + NSTAGE - 1 < c.nt)
                 issue_tile<R>(p, gt, t + NSTAGE - 1, R::stage(lds, t + NSTAGE - 1), idx_lds, wave, lane);
             const uint32_t stage = R::stage(lds, t);
+            // Per-lane fragment offsets, recomputed every tile from a lane id
+            // the compiler cannot see through (keeps ~20 VGPRs free across the
+            // loop instead of hoisting these invariants and spilling).
+            // Swizzles depend on the row mod 16 and XOR only the low 4 bits of
+            // a chunk index, so each fragment address is one of these bases
+            // plus a compile-time multiple of 256 bytes.
+            int ln = lane;
+            asm volatile("" : "+v"(ln));
+            const int lh = ln >> 5, ln32 = ln & 31, lG = ln >> 4, ln16 = ln & 15;
+            const int ltr = 4 * lh + (ln16 >> 2);
 
             // ---- S^T = K . Q^T for rows row0..row0+31: two independent MFMA
             // chains (even / odd k-steps) in an explicit 4-deep LDS pipeline;
             // the scheduler is fenced per step so at most 4 fragments are live.
             f32x16 sacc0 = f32x16{}, sacc1 = f32x16{};
-            const uint32_t rowa = stage + (row0 + n32) * 1024;
-            const uint32_t rowr = stage + R::KV_BYTES + (row0 + n32) * 128;
+            const uint32_t rowa = stage + (row0 + ln32) * 1024;
+            const uint32_t rowr = stage + R::KV_BYTES + (row0 + ln32) * 128;
+            // QK A operand: row row0 + n32, logical chunk 2*ks + h = 16*(ks >> 3) + (2*(ks & 7) + h)
             uint32_t qa[8], ra[4];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) qa[j] = rowa + qk_off[j];
+            for (int j = 0; j < 8; ++j) qa[j] = rowa + (((2 * j + lh) ^ sw_kv(ln32)) << 4);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) ra[j] = rowr + rp_off[j];
+            for (int j = 0; j < 4; ++j) ra[j] = rowr + (((2 * j + lh) ^ sw_rope(ln32 & 15)) << 4);
             auto kfrag = [&](int ks) -> bf16x8 {
                 return ks < 32 ? lds_load<bf16x8>(qa[ks & 7] + ((ks >> 3) << 8)) : lds_load<bf16x8>(ra[ks - 32]);
             };
@@ -440,7 +434,7 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd_wide(FwdParams p) 
             float mloc = -INFINITY;
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
-                const i32x4 iv = lds_load<i32x4>(idx_lds + 4 * (t * BN + row0 + 8 * q + 4 * h));
+                const i32x4 iv = lds_load<i32x4>(idx_lds + 4 * (t * BN + row0 + 8 * q + 4 * lh));
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
                     const bool valid = (unsigned)iv[j] < (unsigned)L;
@@ -468,12 +462,19 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd_wide(FwdParams p) 
 
             // ---- O^T += V^T . P^T, two k-steps of 16 rows x 16 column blocks,
             // same 4-deep pipeline over the 32 (kk, cb) steps.
-            const uint32_t vrow = stage + (row0 + tr_row) * 1024;
+            // PV A operand (transposed reads): for k-step kk and read rd, row
+            // row0 + 16*kk + 8*rd + 4*h + n16/4, columns 32*cb + 16*(G&1) + 4*(n16&3)
+            // -> logical chunk 4*cb + 2*(G&1) + ((n16&3)>>1) = 16*(cb >> 2) + (4*(cb&3) + ...),
+            // byte 8*(n16&1) within the chunk.
+            const uint32_t vrow = stage + (row0 + ltr) * 1024;
             uint32_t va[2][4];
 #pragma unroll
             for (int rd = 0; rd < 2; ++rd)
 #pragma unroll
-                for (int j = 0; j < 4; ++j) va[rd][j] = vrow + rd * 8 * 1024 + tr_off[rd][j];
+                for (int j = 0; j < 4; ++j)
+                    va[rd][j] = vrow + rd * 8 * 1024 +
+                                (((4 * j + 2 * (lG & 1) + ((ln16 & 3) >> 1)) ^ sw_kv(ltr + 8 * rd)) << 4) +
+                                ((ln16 & 1) << 3);
             auto vfrag = [&](int step) -> bf16x8 {
                 const int kk = step >> 4, cb = step & 15;
                 const uint32_t imm = kk * 16 * 1024 + ((cb >> 2) << 8);
@@ -501,8 +502,14 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd_wide(FwdParams p) 
         if (__builtin_amdgcn_readfirstlane(lds_load<int>(flag_lds)) == 0) break;
     }
 
-    // ---- epilogue
+    // ---- epilogue.  Lane-derived values are recomputed from an opaque lane
+    // id: kept live from the prologue they would be spilled, and each reload
+    // waits (vmcnt(0)) for every output store already issued.
     l_run += __shfl_xor(l_run, 32);
+    int eln = lane;
+    asm volatile("" : "+v"(eln));
+    const int eh = eln >> 5, en32 = eln & 31;
+    const int ehead = c.hgi * (32 * HW) + hw * 32 + en32;
     if constexpr (KW == 2) {
         // kv-wave 1 hands (m_ref, m_true, l, O) to kv-wave 0 of the same head
         // slice through LDS; kv-wave 0 merges (m = max, w = exp(m_k - m)).
@@ -510,12 +517,12 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd_wide(FwdParams p) 
         static_assert(HW * 32 * OX_STRIDE * 4 <= R::IDX_OFF, "exchange fits the ring");
         lds_barrier();                  // every wave is past its last ring read
         const uint32_t ml = lds + R::IDX_OFF;
-        const uint32_t ox = lds + ((hw * 32 + n32) * OX_STRIDE + 4 * h) * 4;
+        const uint32_t ox = lds + ((hw * 32 + en32) * OX_STRIDE + 4 * eh) * 4;
         if (kw == 1) {
-            if (h == 0) {
-                lds_store<float>(ml + 4 * (hw * 32 + n32), m_ref);
-                lds_store<float>(ml + 4 * (64 + hw * 32 + n32), m_true);
-                lds_store<float>(ml + 4 * (128 + hw * 32 + n32), l_run);
+            if (eh == 0) {
+                lds_store<float>(ml + 4 * (hw * 32 + en32), m_ref);
+                lds_store<float>(ml + 4 * (64 + hw * 32 + en32), m_true);
+                lds_store<float>(ml + 4 * (128 + hw * 32 + en32), l_run);
             }
 #pragma unroll
             for (int cb = 0; cb < 16; ++cb)
@@ -527,9 +534,9 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd_wide(FwdParams p) 
         }
         lds_barrier();
         if (kw == 1) return;
-        const float m1 = lds_load<float>(ml + 4 * (hw * 32 + n32));
-        const float t1 = lds_load<float>(ml + 4 * (64 + hw * 32 + n32));
-        const float l1 = lds_load<float>(ml + 4 * (128 + hw * 32 + n32));
+        const float m1 = lds_load<float>(ml + 4 * (hw * 32 + en32));
+        const float t1 = lds_load<float>(ml + 4 * (64 + hw * 32 + en32));
+        const float l1 = lds_load<float>(ml + 4 * (128 + hw * 32 + en32));
         const float mm = fmaxf(m_ref, m1);
         const float w0 = fast_exp2(m_ref - mm), w1 = fast_exp2(m1 - mm);
         l_run = w0 * l_run + w1 * l1;
@@ -551,20 +558,20 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd_wide(FwdParams p) 
     const float m_nat = m_true * kLn2;
     if (p.nsplit == 1) {
         const float inv_l = 1.0f / l_run;  // O and l_run share m_ref
-        uint16_t* orow = p.out + ((int64_t)c.token * p.H + head) * 512 + 4 * h;
+        uint16_t* orow = p.out + ((int64_t)c.token * p.H + ehead) * 512 + 4 * eh;
 #pragma unroll
         for (int cb = 0; cb < 16; ++cb)
 #pragma unroll
             for (int q = 0; q < 4; ++q)
                 store_bf16x4(orow + 32 * cb + 8 * q, oacc[cb][4 * q] * inv_l, oacc[cb][4 * q + 1] * inv_l,
                              oacc[cb][4 * q + 2] * inv_l, oacc[cb][4 * q + 3] * inv_l);
-        if (h == 0) {
-            p.out_max[(int64_t)c.token * p.H + head] = m_nat;
-            p.out_sum[(int64_t)c.token * p.H + head] = l_fin;
+        if (eh == 0) {
+            p.out_max[(int64_t)c.token * p.H + ehead] = m_nat;
+            p.out_sum[(int64_t)c.token * p.H + ehead] = l_fin;
         }
     } else {
-        const int64_t prow = ((int64_t)c.token * p.nsplit + c.sp) * p.H + head;
-        float* orow = p.part_o + prow * 512 + 4 * h;
+        const int64_t prow = ((int64_t)c.token * p.nsplit + c.sp) * p.H + ehead;
+        float* orow = p.part_o + prow * 512 + 4 * eh;
 #pragma unroll
         for (int cb = 0; cb < 16; ++cb)
 #pragma unroll
@@ -572,7 +579,7 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd_wide(FwdParams p) 
                 *reinterpret_cast<f32x4*>(orow + 32 * cb + 8 * q) =
                     f32x4{oacc[cb][4 * q], oacc[cb][4 * q + 1], oacc[cb][4 * q + 2], oacc[cb][4 * q + 3]} *
                     to_true;
-        if (h == 0) {
+        if (eh == 0) {
             p.part_m[prow] = m_nat;
             p.part_l[prow] = l_fin;
         }
@@ -606,6 +613,10 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd_narrow(FwdParams p
     const int head = c.hgi * (16 * HW) + hw * 16 + n16;  // this lane's head
     const int L = p.L;
 
+    // Index loads first: the first gather depends on them, Q only on the
+    // first MFMA.
+    const IdxRegs ids = fetch_indices<kBN>(p, c);
+
     // ---- Q fragments: lane holds Q[head][32*ks + 8*g .. +7]; ks 16, 17 from q_rope.
     bf16x8 qf[18];
     {
@@ -618,7 +629,7 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd_narrow(FwdParams p
     }
 
     const uint32_t idx_lds = lds + R::IDX_OFF;
-    store_indices<kBN>(fetch_indices<kBN>(p, c), c, idx_lds);
+    store_indices(ids, idx_lds);
     lds_barrier();
     const Gather gt = make_gather(p, c.b);
 
@@ -639,15 +650,23 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd_narrow(FwdParams p
 #pragma unroll
     for (int j = 0; j < 8; ++j) tr_off[j] = (((2 * j + ((n16 & 3) >> 1)) ^ sw_kv(tr_row)) << 4) + ((n16 & 1) << 3);
 
-    // ---- running state (log2 units; see kRescaleLog2)
+    // ---- running state (log2 units; see kRestartLog2)
     f32x4 oacc[32];
+    float m_ref = -FLT_MAX;   // reference max of P
+    float m_true = -FLT_MAX;  // exact running max
+    float l_run = 0.f;        // per-lane partial of the head's sum, relative to m_ref
+    const uint32_t flag_lds = lds + R::FLAG_OFF;
+
+    // At most two passes over the range, as in the wide variant.
+#pragma unroll 1
+    for (int pass = 0; pass < 2; ++pass) {
 #pragma unroll
     for (int i = 0; i < 32; ++i) oacc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-    float m_ref = -FLT_MAX;
-    float m_true = -FLT_MAX;
-    float l_run = 0.f;
-
+    l_run = 0.f;
+    if (pass == 1) m_ref = m_true;
+    bool overflow = false;
     if (c.nt > 0) issue_tile<R>(p, gt, 0, R::stage(lds, 0), idx_lds, wave, lane);
+    wait_vmcnt<0>();  // Q and tile 0 (see the wide variant)
 
     for (int t = 0; t < c.nt; ++t) {
         R::wait_tile(t, c.nt);
@@ -655,25 +674,41 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd_narrow(FwdParams p
         if (t + 1 < c.nt) issue_tile<R>(p, gt, t + 1, R::stage(lds, t + 1), idx_lds, wave, lane);
 
         const uint32_t stage = R::stage(lds, t);
-        // ---- S^T = K . Q^T for this wave's rows
-        f32x4 sacc[NSUB];
+        // ---- S^T = K . Q^T for this wave's rows.  Steps run k-step major over
+        // the NSUB subtiles in an explicit 4-deep LDS pipeline (the scheduler is
+        // fenced per step); with one subtile the k-steps alternate between two
+        // accumulators so consecutive MFMAs never depend on each other.
+        constexpr int QK_STEPS = 18 * NSUB;
+        constexpr int NCH = NSUB == 1 ? 2 : 1;
+        f32x4 sacc[NSUB][NCH];
+#pragma unroll
+        for (int s = 0; s < NSUB; ++s)
+#pragma unroll
+            for (int ch = 0; ch < NCH; ++ch) sacc[s][ch] = f32x4{0.f, 0.f, 0.f, 0.f};
+        auto kfrag = [&](int step) -> bf16x8 {
+            const int ks = step / NSUB, s = step % NSUB;
+            const int row = rowbase + 16 * s + n16;
+            return ks < 16 ? lds_load<bf16x8>(stage + row * 1024 + qk_off[ks & 3] + ((ks >> 2) << 8))
+                           : lds_load<bf16x8>(stage + R::KV_BYTES + row * 128 + rp_off[ks - 16]);
+        };
+        {
+            bf16x8 kf[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) kf[j] = kfrag(j);
+#pragma unroll
+            for (int step = 0; step < QK_STEPS; ++step) {
+                const int ks = step / NSUB, s = step % NSUB;
+                const int ch = NCH == 2 ? (ks & 1) : 0;
+                sacc[s][ch] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[step & 3], qf[ks], sacc[s][ch], 0, 0, 0);
+                if (step + 4 < QK_STEPS) kf[step & 3] = kfrag(step + 4);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+        f32x4 sres[NSUB];
 #pragma unroll
         for (int s = 0; s < NSUB; ++s) {
-            sacc[s] = f32x4{0.f, 0.f, 0.f, 0.f};
-            const uint32_t rowa = stage + (rowbase + 16 * s + n16) * 1024;
-#pragma unroll
-            for (int ks = 0; ks < 16; ++ks) {
-                const bf16x8 a = lds_load<bf16x8>(rowa + qk_off[ks & 3] + ((ks >> 2) << 8));
-                sacc[s] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qf[ks], sacc[s], 0, 0, 0);
-            }
-            const uint32_t rowr = stage + R::KV_BYTES + (rowbase + 16 * s + n16) * 128;
-#pragma unroll
-            for (int ks = 0; ks < 2; ++ks) {
-                const bf16x8 a = lds_load<bf16x8>(rowr + rp_off[ks]);
-                sacc[s] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qf[16 + ks], sacc[s], 0, 0, 0);
-            }
-            // keep the scheduler from hoisting the next subtile's 18 fragments
-            __builtin_amdgcn_sched_barrier(0);
+            sres[s] = sacc[s][0];
+            if constexpr (NCH == 2) sres[s] += sacc[s][1];
         }
 
         // ---- scale, mask, online softmax.  Lane holds rows
@@ -686,7 +721,7 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd_narrow(FwdParams p
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const bool valid = (unsigned)iv[r] < (unsigned)L;
-                const float v = valid ? sacc[s][r] * kScoreLog2 : -INFINITY;
+                const float v = valid ? sres[s][r] * kScoreLog2 : -INFINITY;
                 x[s][r] = v;
                 mloc = fmaxf(mloc, v);
             }
@@ -694,56 +729,74 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd_narrow(FwdParams p
         mloc = fmaxf(mloc, __shfl_xor(mloc, 16));
         mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
         m_true = fmaxf(m_true, mloc);
-        const bool need = m_true > m_ref + kRescaleLog2;
-        if (__any(need)) {
-            const float nref = need ? m_true : m_ref;
-            const float alpha = fast_exp2(m_ref - nref);
-            m_ref = nref;
-            l_run *= alpha;
-#pragma unroll
-            for (int i = 0; i < 32; ++i) oacc[i] *= alpha;
-        }
+        if (m_ref == -FLT_MAX) m_ref = m_true;  // first valid rows: O and l are still zero
+        overflow |= m_true > m_ref + kRestartLog2;
         float psum = 0.f;
         bf16x4 pb[NSUB];
 #pragma unroll
         for (int s = 0; s < NSUB; ++s) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const float e = fast_exp2(x[s][r] - m_ref);
+                const float e = fast_exp2(fminf(x[s][r] - m_ref, kRestartLog2));
                 psum += e;
                 pb[s][r] = (__bf16)e;
             }
         }
         l_run += psum;
 
-        // ---- O^T += V^T . P^T
+        // ---- O^T += V^T . P^T, one MFMA per (k-step, column block) in an
+        // explicit LDS pipeline (PV_DEPTH fragments in flight).
         if constexpr (NSUB >= 2) {
+            constexpr int PV_STEPS = (NSUB / 2) * 32;
+            constexpr int PV_DEPTH = 4;
+            bf16x8 pk[NSUB / 2];
 #pragma unroll
-            for (int k = 0; k < NSUB / 2; ++k) {
-                const bf16x8 pk = __builtin_shufflevector(pb[2 * k], pb[2 * k + 1], 0, 1, 2, 3, 4, 5, 6, 7);
+            for (int k = 0; k < NSUB / 2; ++k)
+                pk[k] = __builtin_shufflevector(pb[2 * k], pb[2 * k + 1], 0, 1, 2, 3, 4, 5, 6, 7);
+            auto vfrag = [&](int step) -> bf16x8 {
+                const int k = step >> 5, cb = step & 31;
                 const uint32_t r0a = stage + (rowbase + 32 * k + tr_row) * 1024;
-                const uint32_t r1a = r0a + 16 * 1024;
+                const uint32_t pc = tr_off[cb & 7] + ((cb >> 3) << 8);
+                const bf16x4 v0 = lds_load_tr(r0a + pc);
+                const bf16x4 v1 = lds_load_tr(r0a + 16 * 1024 + pc);
+                return __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7);
+            };
+            bf16x8 vf[PV_DEPTH];
 #pragma unroll
-                for (int cb = 0; cb < 32; ++cb) {
-                    const uint32_t pc = tr_off[cb & 7] + ((cb >> 3) << 8);
-                    const bf16x4 v0 = lds_load_tr(r0a + pc);
-                    const bf16x4 v1 = lds_load_tr(r1a + pc);
-                    const bf16x8 va = __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7);
-                    oacc[cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pk, oacc[cb], 0, 0, 0);
-                    if ((cb & 7) == 7) __builtin_amdgcn_sched_barrier(0);
-                }
+            for (int j = 0; j < PV_DEPTH; ++j) vf[j] = vfrag(j);
+#pragma unroll
+            for (int step = 0; step < PV_STEPS; ++step) {
+                const int k = step >> 5, cb = step & 31;
+                oacc[cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf[step % PV_DEPTH], pk[k], oacc[cb], 0, 0, 0);
+                if (step + PV_DEPTH < PV_STEPS) vf[step % PV_DEPTH] = vfrag(step + PV_DEPTH);
+                __builtin_amdgcn_sched_barrier(0);
             }
         } else {
+            constexpr int PV_DEPTH = 8;
             const i16x4 pk = __builtin_bit_cast(i16x4, pb[0]);
             const uint32_t r0a = stage + (rowbase + tr_row) * 1024;
+            auto vfrag = [&](int cb) -> i16x4 {
+                return __builtin_bit_cast(i16x4, lds_load_tr(r0a + tr_off[cb & 7] + ((cb >> 3) << 8)));
+            };
+            i16x4 vf[PV_DEPTH];
+#pragma unroll
+            for (int j = 0; j < PV_DEPTH; ++j) vf[j] = vfrag(j);
 #pragma unroll
             for (int cb = 0; cb < 32; ++cb) {
-                const uint32_t pc = tr_off[cb & 7] + ((cb >> 3) << 8);
-                const i16x4 va = __builtin_bit_cast(i16x4, lds_load_tr(r0a + pc));
-                oacc[cb] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, pk, oacc[cb], 0, 0, 0);
-                if ((cb & 7) == 7) __builtin_amdgcn_sched_barrier(0);
+                oacc[cb] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(vf[cb % PV_DEPTH], pk, oacc[cb], 0, 0, 0);
+                if (cb + PV_DEPTH < 32) vf[cb % PV_DEPTH] = vfrag(cb + PV_DEPTH);
+                __builtin_amdgcn_sched_barrier(0);
             }
         }
+    }
+
+    // ---- workgroup vote: does any head need pass 1?
+    if (pass == 1) break;
+    if (threadIdx.x == 0) lds_store<int>(flag_lds, 0);
+    lds_barrier();  // also: every wave is past its last ring read
+    if (__any(overflow) && lane == 0) lds_store<int>(flag_lds, 1);
+    lds_barrier();
+    if (__builtin_amdgcn_readfirstlane(lds_load<int>(flag_lds)) == 0) break;
     }
 
     // ---- epilogue

@@ -128,6 +128,34 @@ def test_every_variant_and_split(config):
     _run_and_check(f"plan-{config}", data, config=config)
 
 
+def _growing_scores_case(seed, B=1, SQ=2, H=128, L=4096, K=2048):
+    """Scores that rise by ~140 log2 units along the slot order (kv rows ramp
+    0 -> 4 in every coordinate, indices sorted ascending).  The first tile's
+    max is far below the final max, so a kernel that fixes its reference max
+    at the first valid tile and clamps P at 2^64 must recompute the range
+    with the exact max (the second pass)."""
+    g = torch.Generator().manual_seed(seed)
+    q = (1.0 + 0.1 * torch.randn(B, SQ, H, 512, generator=g)).bfloat16()
+    ramp = torch.linspace(0.0, 4.0, L).view(1, L, 1, 1)
+    kv = (ramp + 0.1 * torch.randn(B, L, 1, 512, generator=g)).bfloat16()
+    qr = (0.1 * torch.randn(B, SQ, H, 64, generator=g)).bfloat16()
+    kr = (0.1 * torch.randn(B, L, 1, 64, generator=g)).bfloat16()
+    ids = torch.stack([torch.randperm(L, generator=g)[:K].sort().values for _ in range(B * SQ)])
+    return q, kv, qr, kr, ids.view(B, SQ, 1, K).int().contiguous()
+
+
+@pytest.mark.parametrize("config", PLANS_H128, ids=str)
+def test_growing_scores_second_pass(config):
+    data = _growing_scores_case(11)
+    # the construction really spans more than 2^64 between the first 32 slots and the max
+    q, kv, qr, kr, ids = data
+    rows = ids[0, 0, 0].long()
+    s = (kv[0, rows, 0].float() @ q[0, 0, 0].float() + kr[0, rows, 0].float() @ qr[0, 0, 0].float()) / 24.0
+    log2e = 1.4426950408889634
+    assert (s.max() - s[:32].max()).item() * log2e > 80.0
+    _run_and_check(f"growing-{config}", tuple(t.cuda() for t in data), config=config)
+
+
 def _random_case(seed, B, SQ, H, L, K, invalid=0.1, dup=0.1):
     g = torch.Generator().manual_seed(seed)
     q = torch.randn(B, SQ, H, 512, generator=g).bfloat16()
