@@ -6,14 +6,17 @@ A step is one forward call (main kernel + FP32 split merge) over one batch of
 synthetic inputs already resident in HBM.  The default workload is C2, the
 headline decode case (B=8, SQ=1, H=128, L=32768, TOPK=2048).  Steps cycle
 through ``--rotate`` independent input sets so that the gathered rows come
-from HBM rather than from the 256 MB MALL of a previous identical call; the
-warm (single input set) span is reported beside it.
+from HBM rather than from the 256 MB MALL of a previous call (C2, C3: the
+sets' combined gathered rows exceed twice the MALL); the warm (single input
+set) span is reported beside it.
 
-Timing: HIP events recorded on the launch stream around every call and
-between the main kernel and the merge give the device span per call (the
-``value``), the main-kernel duration (for the roofline) and the merge
-duration; ``ms_per_step`` is the host wall clock of the K timed steps between
-two device synchronisations.
+Timing: K calls are launched back to back on one stream between two HIP
+events (device-synchronised on both sides); the elapsed device time over K is
+the span per call (the ``value``).  The main kernel alone and the merge alone
+are timed the same way (K launches each), which gives the main kernel's
+average duration for the roofline.  An event between every launch would add
+its own few microseconds to each interval, so none is recorded inside a
+batch.  ``ms_per_step`` is the host wall clock of the K timed calls.
 
 cpu_baseline: the CPU oracle (oracle/dsa_oracle.py, a restatement of the
 reference's FP32 PyTorch gather+softmax path) timed on this host on a bounded
@@ -48,7 +51,11 @@ PUBLISHED_SPAN_US = {"c2_decode_b8": 74.875}
 # Which roofline binds each configuration.
 BOUND = {"c1_decode_b1": "hbm", "c2_decode_b8": "hbm", "c3_decode_h16_mtp": "hbm",
          "c4_prefill_h16": "mfma", "c5_prefill_h128": "mfma"}
-DEFAULT_ROTATE = {"c1_decode_b1": 16, "c2_decode_b8": 4, "c3_decode_h16_mtp": 1,
+# Input sets cycled per workload.  C2 and C3 are HBM-bound headlines: their
+# sets' combined gathered rows exceed twice the 256 MB MALL (C2: 32 x 18.9 MB,
+# C3: 2 x 302 MB), so a set's rows have left the MALL when it comes round
+# again.  C4 and C5 are cache-resident by design (9 MiB / 36 MiB of kv).
+DEFAULT_ROTATE = {"c1_decode_b1": 16, "c2_decode_b8": 32, "c3_decode_h16_mtp": 2,
                   "c4_prefill_h16": 1, "c5_prefill_h128": 1}
 
 
@@ -99,29 +106,40 @@ class Call:
             _lib.check(rc, "dsa_merge")
 
 
+def _batch_us(calls, steps, stream_obj, work):
+    """Device time per call of ``steps`` back-to-back launches between two
+    HIP events on the launch stream (no event inside the batch, so the
+    per-event cost of a few microseconds is not charged to every call)."""
+    stream = ctypes.c_void_p(stream_obj.cuda_stream)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record(stream_obj)
+    for i in range(steps):
+        work(calls[i % len(calls)], stream)
+    e1.record(stream_obj)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / steps
+
+
 def time_calls(calls, steps, warmup):
+    """W untimed warm-up calls, then exactly K timed calls (main kernel +
+    merge) back to back between two HIP events, with device synchronisation
+    on both sides: returns (host wall seconds of those K calls, span µs per
+    call).  Then K main-kernel launches alone and K merges alone, timed the
+    same way: (main µs, merge µs) per launch, the main kernel's average
+    duration being the roofline's denominator."""
     stream_obj = torch.cuda.current_stream()
     stream = ctypes.c_void_p(stream_obj.cuda_stream)
+    both = lambda c, s: (c.main(s), c.merge(s))  # noqa: E731
     for i in range(warmup):
-        c = calls[i % len(calls)]
-        c.main(stream)
-        c.merge(stream)
-    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
+        both(calls[i % len(calls)], stream)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for i in range(steps):
-        c = calls[i % len(calls)]
-        ev[i][0].record(stream_obj)
-        c.main(stream)
-        ev[i][1].record(stream_obj)
-        c.merge(stream)
-        ev[i][2].record(stream_obj)
-    torch.cuda.synchronize()
+    span = _batch_us(calls, steps, stream_obj, both)
     wall = time.perf_counter() - t0
-    main_ms = [e[0].elapsed_time(e[1]) for e in ev]
-    merge_ms = [e[1].elapsed_time(e[2]) for e in ev]
-    span_ms = [e[0].elapsed_time(e[2]) for e in ev]
-    return wall, main_ms, merge_ms, span_ms
+    main = _batch_us(calls, steps, stream_obj, lambda c, s: c.main(s))
+    merge = _batch_us(calls, steps, stream_obj, lambda c, s: c.merge(s))
+    return wall, main, merge, span
 
 
 def cpu_baseline(name, data, budget_s=10.0):
@@ -176,11 +194,9 @@ def run(name, args):
     print(f"[bench] {name} shape={shape} plan={config} rotate={rotate}", file=sys.stderr, flush=True)
     sets = [baseline_inputs(name, seed=args.seed + i, device="cuda", cpu_recipe=False) for i in range(rotate)]
     calls = [Call(d, config) for d in sets]
-    wall, main_ms, merge_ms, span_ms = time_calls(calls, args.steps, args.warmup)
-    warm = time_calls(calls[:1], args.steps, args.warmup)
+    wall, main_us, merge_us, span_us = time_calls(calls, args.steps, args.warmup)
+    _, warm_main, _, warm_span = time_calls(calls[:1], args.steps, args.warmup)
     gbytes, flops = algorithmic_units(shape)
-    main_us = statistics.mean(main_ms) * 1e3
-    span_us = statistics.mean(span_ms) * 1e3
     bound = BOUND[name]
     if bound == "hbm":
         achieved, peak, unit = gbytes / (main_us * 1e-6) / 1e9, HBM_PEAK_GBS, "GB/s"
@@ -207,12 +223,11 @@ def run(name, args):
                      "frac": round(achieved / peak, 4), "traffic": traffic_from_profiles(name),
                      "kernel": f"sparse_mla_fwd (main), {gbytes} gathered B and {flops} FLOP per launch"},
         "breakdown": {
-            "span_us_mean": round(span_us, 3),
-            "span_us_median": round(statistics.median(span_ms) * 1e3, 3),
-            "main_us_mean": round(main_us, 3),
-            "merge_us_mean": round(statistics.mean(merge_ms) * 1e3, 3),
-            "warm_span_us_mean": round(statistics.mean(warm[3]) * 1e3, 3),
-            "warm_main_us_mean": round(statistics.mean(warm[1]) * 1e3, 3),
+            "span_us": round(span_us, 3),
+            "main_us": round(main_us, 3),
+            "merge_us": round(merge_us, 3),
+            "warm_span_us": round(warm_span, 3),
+            "warm_main_us": round(warm_main, 3),
             "gathered_TBps_main": round(gbytes / (main_us * 1e-6) / 1e12, 3),
             "mfma_TFLOPs_main": round(flops / (main_us * 1e-6) / 1e12, 2),
             "gathered_TBps_span": round(gbytes / (span_us * 1e-6) / 1e12, 3),

@@ -34,14 +34,10 @@ __global__ __launch_bounds__(256) void merge_kernel(const float* __restrict__ pa
     const int col = (threadIdx.x & 127) * 4;
     const int64_t base = (int64_t)token * nsplit * H + h;  // + s * H
 
+    // One pass: every batch's m, l and u are loaded together (a single round
+    // trip when nsplit <= kBatch, where the result is exactly the two-pass
+    // formula above); later batches fold in with the usual rescale.
     float m = -FLT_MAX;
-    for (int s0 = 0; s0 < nsplit; s0 += kBatch) {
-        float ms[kBatch];
-#pragma unroll
-        for (int j = 0; j < kBatch; ++j) ms[j] = s0 + j < nsplit ? part_m[base + (int64_t)(s0 + j) * H] : -FLT_MAX;
-#pragma unroll
-        for (int j = 0; j < kBatch; ++j) m = fmaxf(m, ms[j]);
-    }
     float l = 0.f;
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
     for (int s0 = 0; s0 < nsplit; s0 += kBatch) {
@@ -55,6 +51,15 @@ __global__ __launch_bounds__(256) void merge_kernel(const float* __restrict__ pa
             ls[j] = live ? part_l[row] : 0.f;
             u[j] = live ? *reinterpret_cast<const f32x4*>(part_o + row * 512 + col) : f32x4{0.f, 0.f, 0.f, 0.f};
         }
+        float mb = m;
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j) mb = fmaxf(mb, ms[j]);
+        if (s0 > 0) {
+            const float alpha = __builtin_amdgcn_exp2f((m - mb) * kLog2e);
+            l *= alpha;
+            acc *= alpha;
+        }
+        m = mb;
 #pragma unroll
         for (int j = 0; j < kBatch; ++j) {
             const float w = __builtin_amdgcn_exp2f((ms[j] - m) * kLog2e);

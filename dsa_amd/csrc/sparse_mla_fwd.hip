@@ -400,10 +400,11 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd_wide(FwdParams p) 
             const int lh = ln >> 5, ln32 = ln & 31, lG = ln >> 4, ln16 = ln & 15;
             const int ltr = 4 * lh + (ln16 >> 2);
 
-            // ---- S^T = K . Q^T for rows row0..row0+31: two independent MFMA
-            // chains (even / odd k-steps) in an explicit 4-deep LDS pipeline;
-            // the scheduler is fenced per step so at most 4 fragments are live.
-            f32x16 sacc0 = f32x16{}, sacc1 = f32x16{};
+            // ---- S^T = K . Q^T for rows row0..row0+31: one MFMA chain (32x32
+            // accumulation chains issue back to back) in an explicit 4-deep LDS
+            // pipeline; the scheduler is fenced per step so at most 4 fragments
+            // are live.
+            f32x16 sacc = f32x16{};
             const uint32_t rowa = stage + (row0 + ln32) * 1024;
             const uint32_t rowr = stage + R::KV_BYTES + (row0 + ln32) * 128;
             // QK A operand: row row0 + n32, logical chunk 2*ks + h = 16*(ks >> 3) + (2*(ks & 7) + h)
@@ -420,43 +421,51 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd_wide(FwdParams p) 
             for (int j = 0; j < 4; ++j) kf[j] = kfrag(j);
 #pragma unroll
             for (int ks = 0; ks < 36; ++ks) {
-                if (ks & 1)
-                    sacc1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[ks & 3], qf[ks], sacc1, 0, 0, 0);
-                else
-                    sacc0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[ks & 3], qf[ks], sacc0, 0, 0, 0);
+                sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[ks & 3], qf[ks], sacc, 0, 0, 0);
                 if (ks + 4 < 36) kf[ks & 3] = kfrag(ks + 4);
                 __builtin_amdgcn_sched_barrier(0);
             }
 
             // ---- scale, mask, online softmax.  Lane holds rows
             // row0 + 8*q + 4*h + (0..3) for q = 0..3 (register 4q + j) of head n32.
+            // Raw scores with masked rows at -inf; the scale folds into the max
+            // (positive factor: max(c*s) = c*max(s)) and into one FMA per
+            // score for P = exp2(c*s - m_ref).
             float x[16];
-            float mloc = -INFINITY;
+            float smax = -INFINITY;
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 const i32x4 iv = lds_load<i32x4>(idx_lds + 4 * (t * BN + row0 + 8 * q + 4 * lh));
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
                     const bool valid = (unsigned)iv[j] < (unsigned)L;
-                    const float sv = sacc0[4 * q + j] + sacc1[4 * q + j];
-                    const float v = valid ? sv * kScoreLog2 : -INFINITY;
-                    x[4 * q + j] = v;
-                    mloc = fmaxf(mloc, v);
+                    x[4 * q + j] = valid ? sacc[4 * q + j] : -INFINITY;
+                    smax = fmaxf(smax, x[4 * q + j]);
                 }
             }
-            mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
-            m_true = fmaxf(m_true, mloc);
+            smax = fmaxf(smax, __shfl_xor(smax, 32));
+            m_true = fmaxf(m_true, smax * kScoreLog2);
             if (m_ref == -FLT_MAX) m_ref = m_true;  // first valid rows: O and l are still zero
-            overflow |= m_true > m_ref + kRestartLog2;
-            // P <= 2^kRestartLog2 unless this pass is to be discarded; the
-            // clamp keeps a discarded pass free of inf.
+            const bool ovf = m_true > m_ref + kRestartLog2;
+            overflow |= ovf;
+            const float neg_ref = -m_ref;
             bf16x8 pk[2];
             float psum = 0.f;
+            if (__any(ovf)) {
+                // This pass is to be discarded; the clamp keeps it free of inf.
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const float e = fast_exp2(fminf(x[r] - m_ref, kRestartLog2));
-                psum += e;
-                pk[r >> 3][r & 7] = (__bf16)e;
+                for (int r = 0; r < 16; ++r) {
+                    const float e = fast_exp2(fminf(fmaf(x[r], kScoreLog2, neg_ref), kRestartLog2));
+                    psum += e;
+                    pk[r >> 3][r & 7] = (__bf16)e;
+                }
+            } else {  // every P <= 2^kRestartLog2
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const float e = fast_exp2(fmaf(x[r], kScoreLog2, neg_ref));
+                    psum += e;
+                    pk[r >> 3][r & 7] = (__bf16)e;
+                }
             }
             l_run += psum;
 
@@ -713,34 +722,48 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd_narrow(FwdParams p
 
         // ---- scale, mask, online softmax.  Lane holds rows
         // rowbase + 16*s + 4*g + r (r = 0..3) of head n16.
+        // Raw scores with masked rows at -inf; the scale folds into the max
+        // and into one FMA per score (see the wide variant).
         float x[NSUB][4];
-        float mloc = -INFINITY;
+        float smax = -INFINITY;
 #pragma unroll
         for (int s = 0; s < NSUB; ++s) {
             const i32x4 iv = lds_load<i32x4>(idx_lds + 4 * (t * kBN + rowbase + 16 * s + 4 * g));
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const bool valid = (unsigned)iv[r] < (unsigned)L;
-                const float v = valid ? sres[s][r] * kScoreLog2 : -INFINITY;
-                x[s][r] = v;
-                mloc = fmaxf(mloc, v);
+                x[s][r] = valid ? sres[s][r] : -INFINITY;
+                smax = fmaxf(smax, x[s][r]);
             }
         }
-        mloc = fmaxf(mloc, __shfl_xor(mloc, 16));
-        mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
-        m_true = fmaxf(m_true, mloc);
+        smax = fmaxf(smax, __shfl_xor(smax, 16));
+        smax = fmaxf(smax, __shfl_xor(smax, 32));
+        m_true = fmaxf(m_true, smax * kScoreLog2);
         if (m_ref == -FLT_MAX) m_ref = m_true;  // first valid rows: O and l are still zero
-        overflow |= m_true > m_ref + kRestartLog2;
+        const bool ovf = m_true > m_ref + kRestartLog2;
+        overflow |= ovf;
+        const float neg_ref = -m_ref;
         float psum = 0.f;
         bf16x4 pb[NSUB];
+        if (__any(ovf)) {
+            // This pass is to be discarded; the clamp keeps it free of inf.
 #pragma unroll
-        for (int s = 0; s < NSUB; ++s) {
+            for (int s = 0; s < NSUB; ++s)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const float e = fast_exp2(fminf(x[s][r] - m_ref, kRestartLog2));
-                psum += e;
-                pb[s][r] = (__bf16)e;
-            }
+                for (int r = 0; r < 4; ++r) {
+                    const float e = fast_exp2(fminf(fmaf(x[s][r], kScoreLog2, neg_ref), kRestartLog2));
+                    psum += e;
+                    pb[s][r] = (__bf16)e;
+                }
+        } else {  // every P <= 2^kRestartLog2
+#pragma unroll
+            for (int s = 0; s < NSUB; ++s)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const float e = fast_exp2(fmaf(x[s][r], kScoreLog2, neg_ref));
+                    psum += e;
+                    pb[s][r] = (__bf16)e;
+                }
         }
         l_run += psum;
 
