@@ -156,6 +156,27 @@ __device__ __forceinline__ int sw_rope(int r) { return (r >> 1) & 7; }
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Cross-lane reductions over lanes l and l ^ 32 (l ^ 16) with the gfx950
+// VALU lane swaps instead of an LDS permute.  v_permlane32_swap on two copies
+// of v leaves (v[l], v[l ^ 32]) in the pair on every lane; v_permlane16_swap
+// does the same for l ^ 16.
+__device__ __forceinline__ float max_xor32(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float max_xor16(float v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float sum_xor32(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float sum_xor16(float v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 // ------------------------------------------------------------ shared pieces
 template <int BN_, int NSTAGE_>
 struct Ring {
@@ -443,7 +464,7 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd_wide(FwdParams p) 
                     smax = fmaxf(smax, x[4 * q + j]);
                 }
             }
-            smax = fmaxf(smax, __shfl_xor(smax, 32));
+            smax = max_xor32(smax);
             m_true = fmaxf(m_true, smax * kScoreLog2);
             if (m_ref == -FLT_MAX) m_ref = m_true;  // first valid rows: O and l are still zero
             const bool ovf = m_true > m_ref + kRestartLog2;
@@ -514,7 +535,7 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd_wide(FwdParams p) 
     // ---- epilogue.  Lane-derived values are recomputed from an opaque lane
     // id: kept live from the prologue they would be spilled, and each reload
     // waits (vmcnt(0)) for every output store already issued.
-    l_run += __shfl_xor(l_run, 32);
+    l_run = sum_xor32(l_run);
     int eln = lane;
     asm volatile("" : "+v"(eln));
     const int eh = eln >> 5, en32 = eln & 31;
@@ -736,8 +757,7 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd_narrow(FwdParams p
                 smax = fmaxf(smax, x[s][r]);
             }
         }
-        smax = fmaxf(smax, __shfl_xor(smax, 16));
-        smax = fmaxf(smax, __shfl_xor(smax, 32));
+        smax = max_xor32(max_xor16(smax));
         m_true = fmaxf(m_true, smax * kScoreLog2);
         if (m_ref == -FLT_MAX) m_ref = m_true;  // first valid rows: O and l are still zero
         const bool ovf = m_true > m_ref + kRestartLog2;
@@ -823,8 +843,7 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd_narrow(FwdParams p
     }
 
     // ---- epilogue
-    l_run += __shfl_xor(l_run, 16);
-    l_run += __shfl_xor(l_run, 32);
+    l_run = sum_xor32(sum_xor16(l_run));
     int cb_lo = 0, cb_hi = 32;
 
     if constexpr (KW > 1) {
