@@ -30,6 +30,19 @@ class DsaPlan(ctypes.Structure):
     ]
 
 
+class DsaFwdOptions(ctypes.Structure):
+    """Mirror of ``struct dsa_fwd_options``."""
+
+    _fields_ = [
+        ("scale", ctypes.c_float),
+        ("block_size", ctypes.c_int32),
+        ("max_blocks", ctypes.c_int32),
+        ("num_blocks", ctypes.c_int32),
+        ("block_table", ctypes.c_void_p),
+        ("reserved", ctypes.c_int64 * 2),
+    ]
+
+
 SIGNATURES = {
     "dsa_version": (_i32, []),
     "dsa_last_error": (ctypes.c_char_p, []),
@@ -41,6 +54,12 @@ SIGNATURES = {
                        _i32, _i32, _i32, _i32, _i32, ctypes.POINTER(DsaPlan), _vp]),
     "dsa_fwd_main": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                             _i32, _i32, _i32, _i32, _i32, ctypes.POINTER(DsaPlan), _vp]),
+    "dsa_fwd_opts": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                            _i32, _i32, _i32, _i32, _i32, ctypes.POINTER(DsaFwdOptions),
+                            ctypes.POINTER(DsaPlan), _vp]),
+    "dsa_fwd_main_opts": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                                 _i32, _i32, _i32, _i32, _i32, ctypes.POINTER(DsaFwdOptions),
+                                 ctypes.POINTER(DsaPlan), _vp]),
     "dsa_merge": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _vp]),
 }
 

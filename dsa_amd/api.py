@@ -19,7 +19,7 @@ from .config import Tuning, check_tuning, select
 
 HEAD_DIM = 512
 ROPE_DIM = 64
-SCALE = 1.0 / 24.0  # 576 ** -0.5, fixed by the operator contract (README.md:81-83 of the reference)
+SCALE = 1.0 / 24.0  # 576 ** -0.5, the reference's fixed scale (README.md:81-83 of the reference)
 _LDS_BYTES = 2 * 64 * 1152 + 2048 * 4
 
 
@@ -33,36 +33,64 @@ class Launch:
     lds_bytes: int
 
 
-def _check_inputs(q, kv, q_rope, k_rope, indices):
+def _check_inputs(q, kv, q_rope, k_rope, indices, block_table=None):
     """Shape, device, layout and dtype contract (reference: dsa/api.py:18-38).
 
     Checks run in the reference's order (shapes, then device/contiguity, then
-    dtypes) and raise ValueError; index values are never read.
+    dtypes) and raise ValueError; index values are never read.  With a
+    ``block_table`` (paged kv, no reference counterpart) kv and k_rope are
+    block pools ``[num_blocks, block_size, 1, 512 / 64]``, ``block_table`` is
+    int32 ``[B, max_blocks]`` and the logical length is
+    ``L = max_blocks * block_size``.
     """
     q_shape, kv_shape, ids_shape = tuple(q.shape), tuple(kv.shape), tuple(indices.shape)
     if len(q_shape) != 4 or len(kv_shape) != 4 or len(ids_shape) != 4:
         raise ValueError("q, kv and indices must be 4-D tensors")
     batch, queries, heads, width = q_shape
-    length, topk = kv_shape[1], ids_shape[-1]
-    if (width != HEAD_DIM or kv_shape != (batch, length, 1, HEAD_DIM)
+    topk = ids_shape[-1]
+    if block_table is None:
+        length = kv_shape[1]
+        pool = (batch, length)
+    else:
+        if block_table.dim() != 2 or block_table.shape[0] != batch:
+            raise ValueError("block_table must be [B, max_blocks]")
+        pool = kv_shape[:2]
+        length = block_table.shape[1] * kv_shape[1]
+    if (width != HEAD_DIM or kv_shape != (*pool, 1, HEAD_DIM)
             or tuple(q_rope.shape) != (batch, queries, heads, ROPE_DIM)
-            or tuple(k_rope.shape) != (batch, length, 1, ROPE_DIM)
+            or tuple(k_rope.shape) != (*pool, 1, ROPE_DIM)
             or ids_shape != (batch, queries, 1, topk)
-            or min(batch, queries, heads, length, topk) <= 0):
-        raise ValueError("expected q[B,SQ,H,512], kv[B,L,1,512], q_rope[B,SQ,H,64], "
-                         "k_rope[B,L,1,64], indices[B,SQ,1,K]")
+            or min(batch, queries, heads, length, topk, *pool) <= 0):
+        if block_table is None:
+            raise ValueError("expected q[B,SQ,H,512], kv[B,L,1,512], q_rope[B,SQ,H,64], "
+                             "k_rope[B,L,1,64], indices[B,SQ,1,K]")
+        raise ValueError("expected q[B,SQ,H,512], kv[N,BS,1,512], q_rope[B,SQ,H,64], "
+                         "k_rope[N,BS,1,64], indices[B,SQ,1,K], block_table[B,M]")
     if heads % 16:
         raise ValueError(f"the number of heads must be a multiple of 16 (got {heads})")
     device = q.device
+    tensors = (kv, q_rope, k_rope, indices) + (() if block_table is None else (block_table,))
     if (device.type != "cuda" or torch.version.hip is None
-            or any(t.device != device for t in (kv, q_rope, k_rope, indices))
-            or not all(t.is_contiguous() for t in (q, kv, q_rope, k_rope, indices))):
+            or any(t.device != device for t in tensors)
+            or not all(t.is_contiguous() for t in (q,) + tensors)):
         raise ValueError("all inputs must be contiguous and on the same ROCm GPU")
     bf16 = torch.bfloat16
     if (q.dtype != bf16 or kv.dtype != bf16 or q_rope.dtype != bf16 or k_rope.dtype != bf16
-            or indices.dtype != torch.int32):
-        raise ValueError("q/kv/q_rope/k_rope must be bfloat16 and indices int32")
+            or indices.dtype != torch.int32
+            or (block_table is not None and block_table.dtype != torch.int32)):
+        raise ValueError("q/kv/q_rope/k_rope must be bfloat16 and indices (and block_table) int32")
     return (batch, queries, heads, length, topk), device
+
+
+def _check_scale(scale):
+    if scale is None:
+        return None
+    if isinstance(scale, bool) or not isinstance(scale, (int, float)):
+        raise TypeError("scale must be a float")
+    scale = float(scale)
+    if not (scale > 0.0 and scale < float("inf")):
+        raise ValueError(f"scale must be a positive finite number (got {scale})")
+    return scale
 
 
 def plan_call(shape, config=None, cores: int = 256):
@@ -88,21 +116,31 @@ def plan_call(shape, config=None, cores: int = 256):
     return config, partials, tuple(launches)
 
 
-def forward(q, kv, q_rope, k_rope, indices, *, config=None, cores=None, return_kernels=False):
+def forward(q, kv, q_rope, k_rope, indices, *, config=None, cores=None, return_kernels=False,
+            scale=None, block_table=None):
     """Sparse MLA attention over given top-k indices.
 
     Returns ``(output, softmax_max, softmax_sum)``: bf16 ``[B,SQ,H,512]`` and
     two fp32 ``[B,1,SQ,H]`` tensors (max and sum of exp(score - max), not LSE).
-    The scale is fixed at 1/24.  Duplicate indices keep their weight; indices
-    outside ``[0, L)`` are masked; every query needs at least one valid index.
+    The scale is 1/24 as in the reference unless ``scale`` is given.
+    Duplicate indices keep their weight; indices outside ``[0, L)`` are masked;
+    every query needs at least one valid index.
 
     ``config``: a :class:`dsa_amd.Tuning` (default: the shape's table entry or
     the library planner).  ``cores``: CU budget for planning (default: the
     device's CU count).  ``return_kernels=True`` also returns the launch
     descriptors.  Outputs are fresh tensors; nothing is cached across calls and
     the call does not synchronise.
+
+    Beyond the reference: ``scale`` (positive float) replaces the fixed 1/24,
+    and ``block_table`` (int32 ``[B, max_blocks]``) selects paged kv, with kv
+    and k_rope given as block pools ``[num_blocks, block_size, 1, 512 / 64]``;
+    logical row ``I`` of batch ``b`` is pool row
+    ``block_table[b, I // block_size] * block_size + I % block_size`` and a
+    slot whose block entry is outside ``[0, num_blocks)`` is masked.
     """
-    shape, device = _check_inputs(q, kv, q_rope, k_rope, indices)
+    scale = _check_scale(scale)
+    shape, device = _check_inputs(q, kv, q_rope, k_rope, indices, block_table)
     if cores is None:
         cores = torch.cuda.get_device_properties(device).multi_processor_count
     config, partials, launches = plan_call(shape, config, cores)
@@ -123,11 +161,21 @@ def forward(q, kv, q_rope, k_rope, indices, *, config=None, cores=None, return_k
 
     plan = config.to_c()
     stream = torch.cuda.current_stream(device).cuda_stream
-    with torch.cuda.device(device):
-        rc = _lib.load().dsa_fwd(
-            ptr(q), ptr(kv), ptr(q_rope), ptr(k_rope), ptr(indices),
+    args = (ptr(q), ptr(kv), ptr(q_rope), ptr(k_rope), ptr(indices),
             ptr(output), ptr(maximum), ptr(denominator), ptr(part_o), ptr(part_m), ptr(part_l),
-            batch, queries, heads, length, topk, ctypes.byref(plan), ctypes.c_void_p(stream))
+            batch, queries, heads, length, topk)
+    with torch.cuda.device(device):
+        if scale is None and block_table is None:
+            rc = _lib.load().dsa_fwd(*args, ctypes.byref(plan), ctypes.c_void_p(stream))
+        else:
+            opts = _lib.DsaFwdOptions()
+            opts.scale = 0.0 if scale is None else scale
+            if block_table is not None:
+                opts.block_size = kv.shape[1]
+                opts.max_blocks = block_table.shape[1]
+                opts.num_blocks = kv.shape[0]
+                opts.block_table = block_table.data_ptr()
+            rc = _lib.load().dsa_fwd_opts(*args, ctypes.byref(opts), ctypes.byref(plan), ctypes.c_void_p(stream))
     _lib.check(rc, "dsa_fwd")
     result = (output, maximum, denominator)
     if return_kernels:

@@ -6,6 +6,7 @@
 // main-kernel + merge launch pair).  The ABI never throws and never allocates.
 #include <hip/hip_runtime_api.h>
 
+#include <cmath>
 #include <cstdarg>
 #include <cstdint>
 #include <cstdio>
@@ -137,10 +138,37 @@ namespace {
 // main kernel and, when `with_merge` and split > 1, the merge.
 int fwd_impl(const uint16_t* q, const uint16_t* kv, const uint16_t* q_rope, const uint16_t* k_rope,
              const int32_t* idx, uint16_t* out, float* out_max, float* out_sum, float* part_o, float* part_m,
-             float* part_l, int B, int SQ, int H, int L, int TOPK, const dsa_plan* plan, hipStream_t stream,
-             bool with_merge) {
+             float* part_l, int B, int SQ, int H, int L, int TOPK, const dsa_fwd_options* opts,
+             const dsa_plan* plan, hipStream_t stream, bool with_merge) {
     if (!q || !kv || !q_rope || !k_rope || !idx) return fail(-1, "NULL input pointer");
     if (int rc = check_shape(B, SQ, H, L, TOPK)) return rc;
+    // Options: scale in log2 units (the default is the reference's 1/24) and
+    // the paged-kv geometry.
+    float scale_log2 = (float)(1.4426950408889634 / 24.0);
+    const int32_t* block_table = nullptr;
+    int block_size = 0, max_blocks = 0, kv_rows = L;
+    if (opts) {
+        if (opts->scale != 0.0f) {
+            if (!(opts->scale > 0.0f) || !std::isfinite(opts->scale))
+                return fail(-1, "scale must be a positive finite number (got %g)", (double)opts->scale);
+            scale_log2 = (float)((double)opts->scale * 1.4426950408889634);
+        }
+        if (opts->block_table) {
+            block_table = opts->block_table;
+            block_size = opts->block_size;
+            max_blocks = opts->max_blocks;
+            if (block_size <= 0 || max_blocks <= 0 || opts->num_blocks <= 0)
+                return fail(-1, "block_size, max_blocks and num_blocks must be positive (got %d, %d, %d)",
+                            block_size, max_blocks, opts->num_blocks);
+            if ((int64_t)max_blocks * block_size != L)
+                return fail(-1, "L must equal max_blocks * block_size (%d != %d * %d)", L, max_blocks, block_size);
+            if ((int64_t)opts->num_blocks * block_size >= (1 << 22))
+                return fail(-1, "num_blocks * block_size must be below 4194304 (got %lld)",
+                            (long long)opts->num_blocks * block_size);
+            if ((uintptr_t)block_table & 3) return fail(-1, "block_table must be 4-byte aligned");
+            kv_rows = opts->num_blocks * block_size;
+        }
+    }
     dsa_plan local{};
     if (!plan) {
         if (!with_merge) return fail(-1, "dsa_fwd_main needs an explicit plan");
@@ -182,6 +210,11 @@ int fwd_impl(const uint16_t* q, const uint16_t* kv, const uint16_t* q_rope, cons
     p.H = H;
     p.L = L;
     p.TOPK = TOPK;
+    p.score_scale_log2 = scale_log2;
+    p.block_table = block_table;
+    p.block_size = block_size;
+    p.max_blocks = max_blocks;
+    p.kv_rows = kv_rows;
     p.nsplit = plan->split;
     p.ntiles = ceil_div(TOPK, plan->tile_rows);
     p.hgroups = H / plan->heads_per_group;
@@ -206,7 +239,7 @@ int dsa_fwd(const uint16_t* q, const uint16_t* kv, const uint16_t* q_rope, const
             const int32_t* idx, uint16_t* out, float* out_max, float* out_sum, float* part_o, float* part_m,
             float* part_l, int B, int SQ, int H, int L, int TOPK, const dsa_plan* plan, hipStream_t stream) {
     return fwd_impl(q, kv, q_rope, k_rope, idx, out, out_max, out_sum, part_o, part_m, part_l, B, SQ, H, L,
-                    TOPK, plan, stream, true);
+                    TOPK, nullptr, plan, stream, true);
 }
 
 int dsa_fwd_main(const uint16_t* q, const uint16_t* kv, const uint16_t* q_rope, const uint16_t* k_rope,
@@ -214,7 +247,23 @@ int dsa_fwd_main(const uint16_t* q, const uint16_t* kv, const uint16_t* q_rope, 
                  float* part_m, float* part_l, int B, int SQ, int H, int L, int TOPK, const dsa_plan* plan,
                  hipStream_t stream) {
     return fwd_impl(q, kv, q_rope, k_rope, idx, out, out_max, out_sum, part_o, part_m, part_l, B, SQ, H, L,
-                    TOPK, plan, stream, false);
+                    TOPK, nullptr, plan, stream, false);
+}
+
+int dsa_fwd_opts(const uint16_t* q, const uint16_t* kv, const uint16_t* q_rope, const uint16_t* k_rope,
+                 const int32_t* idx, uint16_t* out, float* out_max, float* out_sum, float* part_o, float* part_m,
+                 float* part_l, int B, int SQ, int H, int L, int TOPK, const dsa_fwd_options* opts,
+                 const dsa_plan* plan, hipStream_t stream) {
+    return fwd_impl(q, kv, q_rope, k_rope, idx, out, out_max, out_sum, part_o, part_m, part_l, B, SQ, H, L,
+                    TOPK, opts, plan, stream, true);
+}
+
+int dsa_fwd_main_opts(const uint16_t* q, const uint16_t* kv, const uint16_t* q_rope, const uint16_t* k_rope,
+                      const int32_t* idx, uint16_t* out, float* out_max, float* out_sum, float* part_o,
+                      float* part_m, float* part_l, int B, int SQ, int H, int L, int TOPK,
+                      const dsa_fwd_options* opts, const dsa_plan* plan, hipStream_t stream) {
+    return fwd_impl(q, kv, q_rope, k_rope, idx, out, out_max, out_sum, part_o, part_m, part_l, B, SQ, H, L,
+                    TOPK, opts, plan, stream, false);
 }
 
 }  // extern "C"

@@ -11,9 +11,9 @@ namespace dsa {
 // kernel argument block.
 struct FwdParams {
     const uint16_t* q;       // [tokens, H, 512] bf16
-    const uint16_t* kv;      // [B, L, 512] bf16
+    const uint16_t* kv;      // [B, L, 512] bf16, or a [kv_rows, 512] pool when paged
     const uint16_t* q_rope;  // [tokens, H, 64] bf16
-    const uint16_t* k_rope;  // [B, L, 64] bf16
+    const uint16_t* k_rope;  // [B, L, 64] bf16, or a [kv_rows, 64] pool when paged
     const int32_t* idx;      // [tokens, TOPK] int32
     uint16_t* out;           // [tokens, H, 512] bf16        (nsplit == 1)
     float* out_max;          // [tokens, H]                  (nsplit == 1)
@@ -22,6 +22,13 @@ struct FwdParams {
     float* part_m;           // [tokens, nsplit, H]          (nsplit > 1)
     float* part_l;           // [tokens, nsplit, H]          (nsplit > 1)
     int B, SQ, H, L, TOPK;
+    float score_scale_log2;  // softmax scale * log2(e) (the reference fixes the scale at 1/24)
+    // Paged kv (NULL block_table: contiguous [B, L] rows).  Row I of batch b
+    // is pool row block_table[b * max_blocks + I / block_size] * block_size
+    // + I % block_size; kv and k_rope are then pools of kv_rows rows.
+    const int32_t* block_table;
+    int block_size, max_blocks;
+    int kv_rows;             // rows one gather may address: L (contiguous) or the pool size
     int nsplit;              // KV splits per (token, head group)
     int ntiles;              // ceil(TOPK / tile_rows)
     int hgroups;             // H / heads_per_group

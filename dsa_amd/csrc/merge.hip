@@ -19,7 +19,7 @@ typedef __attribute__((__vector_size__(4 * sizeof(__bf16)))) __bf16 bf16x4;
 
 constexpr float kLog2e = 1.4426950408889634f;
 
-constexpr int kBatch = 8;  // split partials loaded per batch (kept in flight together)
+constexpr int kBatch = 16;  // split partials loaded per batch (kept in flight together)
 
 __global__ __launch_bounds__(256) void merge_kernel(const float* __restrict__ part_o,
                                                     const float* __restrict__ part_m,

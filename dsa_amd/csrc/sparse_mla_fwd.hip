@@ -1,12 +1,12 @@
 // Sparse-MLA attention forward for gfx950 (MI355X).
 //
 // One workgroup (4 waves) owns (token, KV split, head group).  It gathers the
-// selected 576-wide rows (kv[:512] ++ k_rope[:64]) straight from HBM into a
-// two-stage LDS ring with global_load_lds_dwordx4 (no VGPR staging); every
-// wave then computes, for its slice of heads and rows,
+// selected 576-wide rows (kv[:512] ++ k_rope[:64]) straight from HBM into an
+// LDS ring with buffer_load_dwordx4 ... lds (no VGPR staging); every wave then
+// computes, for its slice of heads and rows,
 //
 //   S^T[row, head] = K[row, :576] . Q[head, :576]       A = K from LDS, B = Q in VGPRs
-//   online softmax over rows in registers (log2 units, FP32 state)
+//   softmax over rows in registers (log2 units, FP32 state)
 //   O^T[col, head] += V^T[col, row] . P^T[row, head]    A = V read with ds_read_b64_tr_b16,
 //                                                        B = P in VGPRs
 //
@@ -15,19 +15,20 @@
 // share one gathered tile.  Two variants:
 //
 //   wide   -- v_mfma_f32_32x32x16_bf16, 32 heads per wave (Q: 144 VGPRs,
-//             O: 256 accumulators), 2 head-waves x 2 row-waves = 64 heads per
-//             workgroup.  Twice the operand reuse per LDS byte of the narrow
-//             variant and the full-rate MFMA on gfx950.
-//   narrow -- v_mfma_f32_16x16x32_bf16, 16 heads per wave; for head counts
-//             that are not a multiple of 64 (H = 16, 32, 48, ...).
+//             O: 256 accumulators): 4 head-waves = 128 heads per workgroup on
+//             32-row tiles (4-stage ring), or 2 head-waves x 2 row-waves = 64
+//             heads on 64-row tiles.
+//   narrow -- v_mfma_f32_16x16x32_bf16, 16 heads per wave: 64, 32 or 16 heads
+//             per workgroup with 1, 2 or 4 row-waves on 64-row tiles.
 //
 // Math follows the reference workspace kernel (dsa/workspace.py:242-390):
 // running max initialised to -FLT_MAX (:68), scores scaled and masked by the
-// raw index (:252-257), FP32 sum of the FP32 exponentials, P rounded to bf16
+// index (:252-257), FP32 sum of the FP32 exponentials, P rounded to bf16
 // (RNE) before PV (:270-272), FP32 accumulation, and for split > 1 the
 // unnormalised FP32 numerator plus (max, sum) partials (:379-385).  Scores are
-// carried in log2 units (x * log2(e)/24) so that every exponential is one
-// v_exp_f32; max/sum leave the kernel in natural units.
+// carried in log2 units (x * scale * log2(e); the reference's scale is 1/24)
+// so that every exponential is one v_exp_f32; max/sum leave the kernel in
+// natural units.
 #include <hip/hip_runtime.h>
 #include <float.h>
 #include <stdint.h>
@@ -47,7 +48,6 @@ typedef __attribute__((__vector_size__(4 * sizeof(int)))) int i32x4;
 
 // log2(e) / 24: multiplying the raw QK dot product by this gives the score in
 // log2 units, so exp(score - max) == exp2(x - x_max).
-constexpr float kScoreLog2 = (float)(1.4426950408889634 / 24.0);
 constexpr float kLn2 = 0.69314718055994531f;
 // P is formed against a reference max m_ref fixed at the first tile with a
 // valid row and is clamped at 2^kRestartLog2; a head whose running max exceeds
@@ -247,28 +247,58 @@ __device__ __forceinline__ WgCoords wg_coords(const FwdParams& p) {
     return c;
 }
 
-// Indices of the workgroup's slot range, padded with -1 so a ragged last
-// tile is masked (nslots <= DSA_IDX_CAP, checked on the host).  Split into a
-// global-load half and an LDS-store half so other loads can be issued in
-// between without waiting for these.
+// Rows of the workgroup's slot range, -1 for every masked slot (including
+// the padding of a ragged last tile; nslots <= DSA_IDX_CAP, checked on the
+// host).  Split into a global-load half and an LDS-store half so other loads
+// can be issued in between without waiting for these.
 struct IdxRegs {
     int v[DSA_IDX_CAP / kThreads];
 };
 template <int BN>
 __device__ __forceinline__ IdxRegs fetch_indices(const FwdParams& p, const WgCoords& c) {
     // Buffer loads over the token's index row: a slot past TOPK reads 0
-    // (hardware range check) and is then masked to -1.  Being intrinsics
-    // rather than plain loads, they are never turned into branches around
-    // each load, so all of them issue back to back.
+    // (hardware range check) and is then masked.  Being intrinsics rather
+    // than plain loads, they are never turned into branches around each load,
+    // so all of them issue back to back.
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<int32_t*>(p.idx + (int64_t)c.token * p.TOPK), (short)0, p.TOPK * 4, 0x00020000);
     const int nslots = c.nt * BN;
-    IdxRegs r;
+    int raw[DSA_IDX_CAP / kThreads];
 #pragma unroll
-    for (int i = 0; i < DSA_IDX_CAP / kThreads; ++i) {
-        const int s = (int)threadIdx.x + i * kThreads;
-        const int v = __builtin_amdgcn_raw_buffer_load_b32(rs, (c.slot0 + s) * 4, 0, 0);
-        r.v[i] = ((s < nslots) & (c.slot0 + s < p.TOPK)) ? v : -1;
+    for (int i = 0; i < DSA_IDX_CAP / kThreads; ++i)
+        raw[i] = __builtin_amdgcn_raw_buffer_load_b32(rs, (c.slot0 + (int)threadIdx.x + i * kThreads) * 4, 0, 0);
+    // Cached value: the kv row to gather (the pool row when paged), or -1 for
+    // a masked slot (index < 0 or >= L, slot past TOPK or past the range).
+    IdxRegs r;
+    if (p.block_table == nullptr) {
+#pragma unroll
+        for (int i = 0; i < DSA_IDX_CAP / kThreads; ++i) {
+            const int s = (int)threadIdx.x + i * kThreads;
+            const bool ok = (s < nslots) & (c.slot0 + s < p.TOPK) & (raw[i] >= 0) & (raw[i] < p.L);
+            r.v[i] = ok ? raw[i] : -1;
+        }
+    } else {
+        // Second level: the block table row of this batch (again range
+        // checked by the buffer descriptor; an entry outside the pool masks
+        // the slot).
+        const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<int32_t*>(p.block_table + (int64_t)c.b * p.max_blocks), (short)0, p.max_blocks * 4,
+            0x00020000);
+        int blk[DSA_IDX_CAP / kThreads];
+#pragma unroll
+        for (int i = 0; i < DSA_IDX_CAP / kThreads; ++i) {
+            const int id = min(max(raw[i], 0), p.L - 1);
+            blk[i] = __builtin_amdgcn_raw_buffer_load_b32(rb, (id / p.block_size) * 4, 0, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < DSA_IDX_CAP / kThreads; ++i) {
+            const int s = (int)threadIdx.x + i * kThreads;
+            const int id = min(max(raw[i], 0), p.L - 1);
+            const int row = blk[i] * p.block_size + id % p.block_size;
+            const bool ok = (s < nslots) & (c.slot0 + s < p.TOPK) & (raw[i] >= 0) & (raw[i] < p.L) &
+                            (blk[i] >= 0) & (row < p.kv_rows);
+            r.v[i] = ok ? row : -1;
+        }
     }
     return r;
 }
@@ -286,24 +316,24 @@ struct Gather {
     rsrc_t kv, kr;
 };
 __device__ __forceinline__ Gather make_gather(const FwdParams& p, int b) {
-    const int64_t rows = (int64_t)b * p.L;
+    const int64_t rows = p.block_table ? 0 : (int64_t)b * p.L;  // first row of the addressed range
     Gather g;
-    g.kv = make_rsrc(reinterpret_cast<const char*>(p.kv) + rows * 1024, (uint32_t)p.L * 1024u);
-    g.kr = make_rsrc(reinterpret_cast<const char*>(p.k_rope) + rows * 128, (uint32_t)p.L * 128u);
+    g.kv = make_rsrc(reinterpret_cast<const char*>(p.kv) + rows * 1024, (uint32_t)p.kv_rows * 1024u);
+    g.kr = make_rsrc(reinterpret_cast<const char*>(p.k_rope) + rows * 128, (uint32_t)p.kv_rows * 128u);
     return g;
 }
 
 // Gather of workgroup tile t into ring stage `stage` (LDS byte address).
 // Wave w fetches kv rows [w*KV_PER_WAVE, (w+1)*KV_PER_WAVE) (1 KiB each, one
-// instruction per row) and ROPE_PER_WAVE groups of 8 rope rows.  Row indices
-// are clamped to [0, L) for the address; the mask uses the raw index.
+// instruction per row) and ROPE_PER_WAVE groups of 8 rope rows.  A masked
+// slot (-1 in the index cache) gathers row 0; its score is masked later.
 template <class R>
 __device__ __forceinline__ void issue_tile(const FwdParams& p, const Gather& gt, int t, uint32_t stage,
                                            uint32_t idx_lds, int wave, int lane) {
-    const int L = p.L;
+    const int rows = p.kv_rows;
     const int r0 = wave * R::KV_PER_WAVE;
     const int my_id = lds_load<int>(idx_lds + 4 * (t * R::BN + r0 + (lane % R::KV_PER_WAVE)));
-    const uint32_t my_off = (uint32_t)min(max(my_id, 0), L - 1) << 10;
+    const uint32_t my_off = (uint32_t)min(max(my_id, 0), rows - 1) << 10;
     const uint32_t lane16 = (uint32_t)lane << 4;
 #pragma unroll
     for (int rr = 0; rr < R::KV_PER_WAVE; ++rr) {
@@ -316,7 +346,7 @@ __device__ __forceinline__ void issue_tile(const FwdParams& p, const Gather& gt,
         const int j = wave * R::ROPE_PER_WAVE + jj;
         const int r = j * 8 + (lane >> 3);
         const int id = lds_load<int>(idx_lds + 4 * (t * R::BN + r));
-        const uint32_t voff = ((uint32_t)min(max(id, 0), L - 1) << 7) + (((lane & 7) ^ sw_rope(r)) << 4);
+        const uint32_t voff = ((uint32_t)min(max(id, 0), rows - 1) << 7) + (((lane & 7) ^ sw_rope(r)) << 4);
         gather_lanes(stage + R::KV_BYTES + j * 1024, gt.kr, voff);
     }
 }
@@ -354,7 +384,6 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd_wide(FwdParams p) 
 
     const WgCoords c = wg_coords<BN>(p);
     const int head = c.hgi * (32 * HW) + hw * 32 + n32;  // this lane's head
-    const int L = p.L;
     const uint32_t idx_lds = lds + R::IDX_OFF;
 
     // Index loads first: the first gather depends on them, Q only on the
@@ -426,6 +455,11 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd_wide(FwdParams p) 
             // pipeline; the scheduler is fenced per step so at most 4 fragments
             // are live.
             f32x16 sacc = f32x16{};
+            // Slot indices of this lane's 16 score rows (for the mask), read
+            // before the MFMAs so their LDS latency is hidden.
+            i32x4 ivs[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) ivs[q] = lds_load<i32x4>(idx_lds + 4 * (t * BN + row0 + 8 * q + 4 * lh));
             const uint32_t rowa = stage + (row0 + ln32) * 1024;
             const uint32_t rowr = stage + R::KV_BYTES + (row0 + ln32) * 128;
             // QK A operand: row row0 + n32, logical chunk 2*ks + h = 16*(ks >> 3) + (2*(ks & 7) + h)
@@ -456,16 +490,15 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd_wide(FwdParams p) 
             float smax = -INFINITY;
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
-                const i32x4 iv = lds_load<i32x4>(idx_lds + 4 * (t * BN + row0 + 8 * q + 4 * lh));
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
-                    const bool valid = (unsigned)iv[j] < (unsigned)L;
+                    const bool valid = ivs[q][j] >= 0;
                     x[4 * q + j] = valid ? sacc[4 * q + j] : -INFINITY;
                     smax = fmaxf(smax, x[4 * q + j]);
                 }
             }
             smax = max_xor32(smax);
-            m_true = fmaxf(m_true, smax * kScoreLog2);
+            m_true = fmaxf(m_true, smax * p.score_scale_log2);
             if (m_ref == -FLT_MAX) m_ref = m_true;  // first valid rows: O and l are still zero
             const bool ovf = m_true > m_ref + kRestartLog2;
             overflow |= ovf;
@@ -476,14 +509,14 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd_wide(FwdParams p) 
                 // This pass is to be discarded; the clamp keeps it free of inf.
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
-                    const float e = fast_exp2(fminf(fmaf(x[r], kScoreLog2, neg_ref), kRestartLog2));
+                    const float e = fast_exp2(fminf(fmaf(x[r], p.score_scale_log2, neg_ref), kRestartLog2));
                     psum += e;
                     pk[r >> 3][r & 7] = (__bf16)e;
                 }
             } else {  // every P <= 2^kRestartLog2
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
-                    const float e = fast_exp2(fmaf(x[r], kScoreLog2, neg_ref));
+                    const float e = fast_exp2(fmaf(x[r], p.score_scale_log2, neg_ref));
                     psum += e;
                     pk[r >> 3][r & 7] = (__bf16)e;
                 }
@@ -641,7 +674,6 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd_narrow(FwdParams p
 
     const WgCoords c = wg_coords<kBN>(p);
     const int head = c.hgi * (16 * HW) + hw * 16 + n16;  // this lane's head
-    const int L = p.L;
 
     // Index loads first: the first gather depends on them, Q only on the
     // first MFMA.
@@ -708,6 +740,10 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd_narrow(FwdParams p
         // the NSUB subtiles in an explicit 4-deep LDS pipeline (the scheduler is
         // fenced per step); with one subtile the k-steps alternate between two
         // accumulators so consecutive MFMAs never depend on each other.
+        // Slot indices of this lane's score rows, read before the MFMAs.
+        i32x4 ivs[NSUB];
+#pragma unroll
+        for (int s = 0; s < NSUB; ++s) ivs[s] = lds_load<i32x4>(idx_lds + 4 * (t * kBN + rowbase + 16 * s + 4 * g));
         constexpr int QK_STEPS = 18 * NSUB;
         constexpr int NCH = NSUB == 1 ? 2 : 1;
         f32x4 sacc[NSUB][NCH];
@@ -749,16 +785,15 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd_narrow(FwdParams p
         float smax = -INFINITY;
 #pragma unroll
         for (int s = 0; s < NSUB; ++s) {
-            const i32x4 iv = lds_load<i32x4>(idx_lds + 4 * (t * kBN + rowbase + 16 * s + 4 * g));
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const bool valid = (unsigned)iv[r] < (unsigned)L;
+                const bool valid = ivs[s][r] >= 0;
                 x[s][r] = valid ? sres[s][r] : -INFINITY;
                 smax = fmaxf(smax, x[s][r]);
             }
         }
         smax = max_xor32(max_xor16(smax));
-        m_true = fmaxf(m_true, smax * kScoreLog2);
+        m_true = fmaxf(m_true, smax * p.score_scale_log2);
         if (m_ref == -FLT_MAX) m_ref = m_true;  // first valid rows: O and l are still zero
         const bool ovf = m_true > m_ref + kRestartLog2;
         overflow |= ovf;
@@ -771,7 +806,7 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd_narrow(FwdParams p
             for (int s = 0; s < NSUB; ++s)
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    const float e = fast_exp2(fminf(fmaf(x[s][r], kScoreLog2, neg_ref), kRestartLog2));
+                    const float e = fast_exp2(fminf(fmaf(x[s][r], p.score_scale_log2, neg_ref), kRestartLog2));
                     psum += e;
                     pb[s][r] = (__bf16)e;
                 }
@@ -780,7 +815,7 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd_narrow(FwdParams p
             for (int s = 0; s < NSUB; ++s)
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    const float e = fast_exp2(fmaf(x[s][r], kScoreLog2, neg_ref));
+                    const float e = fast_exp2(fmaf(x[s][r], p.score_scale_log2, neg_ref));
                     psum += e;
                     pb[s][r] = (__bf16)e;
                 }

@@ -4,6 +4,7 @@
  * The library computes, for every token t = (b, s) and head h,
  *
  *   score_j = (q[t,h,:512] . kv[b,I_j,:] + q_rope[t,h,:64] . k_rope[b,I_j,:]) / 24
+ *             (scale 1/24 as in the reference; dsa_fwd_opts takes another)
  *   score_j = -inf  when I_j < 0 or I_j >= L            (index masked, slot kept)
  *   max     = max_j score_j
  *   sum     = sum_j exp(score_j - max)                  (FP32 exponentials)
@@ -128,6 +129,52 @@ int dsa_fwd_main(const uint16_t* q, const uint16_t* kv, const uint16_t* q_rope,
                  float* part_o, float* part_m, float* part_l,
                  int B, int SQ, int H, int L, int TOPK,
                  const dsa_plan* plan, hipStream_t stream);
+
+/*
+ * Options beyond the reference's operator contract, which fixes the scale at
+ * 1/24 and takes only contiguous kv (dsa/api.py:18-38, 77-86).  A
+ * zero-initialised struct selects exactly the reference behaviour.
+ *
+ *   scale       : softmax scale applied to q.k (> 0); 0 selects 1/24 = 576^-0.5.
+ *                 Models keep their own scale (e.g. (d_nope + d_rope)^-0.5).
+ *   block_table : paged kv.  NULL: kv [B, L, 1, 512] and k_rope [B, L, 1, 64]
+ *                 as in dsa_fwd.  Otherwise kv is a pool [num_blocks,
+ *                 block_size, 1, 512], k_rope a pool [num_blocks, block_size,
+ *                 1, 64], block_table is int32 [B, max_blocks], and logical
+ *                 row I of batch b is pool row
+ *                 block_table[b * max_blocks + I / block_size] * block_size
+ *                 + I % block_size.  L must equal max_blocks * block_size and
+ *                 num_blocks * block_size must be below 4194304.  Indices stay
+ *                 logical and are masked as in dsa_fwd; a slot whose block
+ *                 entry lies outside [0, num_blocks) is masked as well.
+ */
+typedef struct dsa_fwd_options {
+    float scale;
+    int32_t block_size;
+    int32_t max_blocks;
+    int32_t num_blocks;
+    const int32_t* block_table;
+    int64_t reserved[2];
+} dsa_fwd_options;
+
+/*
+ * dsa_fwd and dsa_fwd_main with options (opts NULL = all defaults).  No
+ * reference counterpart: the softmax scale and paged kv are the next steps
+ * beyond the reference's fixed-scale, contiguous-cache operator.
+ */
+int dsa_fwd_opts(const uint16_t* q, const uint16_t* kv, const uint16_t* q_rope,
+                 const uint16_t* k_rope, const int32_t* idx,
+                 uint16_t* out, float* out_max, float* out_sum,
+                 float* part_o, float* part_m, float* part_l,
+                 int B, int SQ, int H, int L, int TOPK,
+                 const dsa_fwd_options* opts, const dsa_plan* plan, hipStream_t stream);
+
+int dsa_fwd_main_opts(const uint16_t* q, const uint16_t* kv, const uint16_t* q_rope,
+                      const uint16_t* k_rope, const int32_t* idx,
+                      uint16_t* out, float* out_max, float* out_sum,
+                      float* part_o, float* part_m, float* part_l,
+                      int B, int SQ, int H, int L, int TOPK,
+                      const dsa_fwd_options* opts, const dsa_plan* plan, hipStream_t stream);
 
 /*
  * FP32 merge of split partials (dsa/merge.py:13-91):

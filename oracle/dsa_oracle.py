@@ -20,12 +20,20 @@ Functions and the reference code each one restates:
 * ``c_exact`` / ``c_tiled`` -- the C restatement in oracle/dsa_oracle.c:
                          FP64 brute force, and the device-side arithmetic
                          (tiles, bf16 P, FP32 state, split + merge).
+* ``unpage`` / ``mask_unbacked`` -- paged-kv pools to the reference's
+                         contiguous layout (no reference counterpart: the
+                         reference takes contiguous kv only), so paged runs are
+                         checked against the same ``reference``.
+
+``reference(scale=...)`` generalises the fixed 1/24 (tools/review.py:140) to
+another softmax scale; the default keeps the reference's exact division.
 
 Pinning (tests/test_oracle.py): golden statistics of 20 reference validation
 records, both tutorial known-answer tests, reduction to a library
-scaled_dot_product_attention, FP64 brute force, closed forms of the uniform
-family, index-permutation / -1-removal / duplicate-counting invariants, and
-planted mistakes that each check must reject.
+scaled_dot_product_attention (which also pins ``scale``), FP64 brute force,
+closed forms of the uniform family, index-permutation / -1-removal /
+duplicate-counting invariants, an identity block table and a gather
+restatement for ``unpage``, and planted mistakes that each check must reject.
 """
 from __future__ import annotations
 
@@ -41,11 +49,12 @@ HERE = Path(__file__).resolve().parent
 C_LIB = HERE / "_build" / "libdsa_oracle.so"
 
 
-def reference(q, kv, q_rope, k_rope, indices, chunk: int = 16, tokens=None):
+def reference(q, kv, q_rope, k_rope, indices, chunk: int = 16, tokens=None, scale=None):
     """FP32 oracle: returns (output fp32 [B,SQ,H,512], max [B,1,SQ,H], sum [B,1,SQ,H]).
 
     ``tokens``: optional iterable of (b, s) pairs; only those rows are computed
-    (the rest of the outputs stay NaN).
+    (the rest of the outputs stay NaN).  ``scale``: softmax scale (None: the
+    reference's fixed division by 24, tools/review.py:140).
     """
     q, kv, q_rope, k_rope, indices = (t.cpu() for t in (q, kv, q_rope, k_rope, indices))
     batch, queries, heads, _ = q.shape
@@ -69,7 +78,8 @@ def reference(q, kv, q_rope, k_rope, indices, chunk: int = 16, tokens=None):
         selected = kv[bi, index, 0].float()
         rope = k_rope[bi, index, 0].float()
         score = (torch.bmm(q[bi, rows_t].float(), selected.transpose(1, 2))
-                 + torch.bmm(q_rope[bi, rows_t].float(), rope.transpose(1, 2))) / SCALE_DIVISOR
+                 + torch.bmm(q_rope[bi, rows_t].float(), rope.transpose(1, 2)))
+        score = score / SCALE_DIVISOR if scale is None else score * scale
         score.masked_fill_(~valid[:, None, :], -float("inf"))
         maximum = score.amax(-1)
         exponent = (score - maximum[..., None]).exp()
@@ -78,6 +88,35 @@ def reference(q, kv, q_rope, k_rope, indices, chunk: int = 16, tokens=None):
         mx[bi, 0, rows_t] = maximum
         sm[bi, 0, rows_t] = denominator
     return out, mx, sm
+
+
+def unpage(kv_pool, rope_pool, block_table):
+    """Contiguous ``[B, L, 1, D]`` copies of paged kv / k_rope pools
+    ``[num_blocks, block_size, 1, D]`` under ``block_table [B, max_blocks]``
+    (logical row I of batch b = pool row block_table[b, I // block_size] *
+    block_size + I % block_size), and a ``[B, L]`` bool that is False where
+    the block entry lies outside the pool (those rows are masked)."""
+    kv_pool, rope_pool, block_table = (t.cpu() for t in (kv_pool, rope_pool, block_table))
+    blocks, size = kv_pool.shape[:2]
+    rows = torch.arange(block_table.shape[1] * size)
+    blk = block_table[:, rows // size].long()
+    ok = (blk >= 0) & (blk < blocks)
+    flat = blk.clamp(0, blocks - 1) * size + rows % size
+    kv = kv_pool.reshape(blocks * size, 1, -1)[flat]
+    rope = rope_pool.reshape(blocks * size, 1, -1)[flat]
+    return kv, rope, ok
+
+
+def mask_unbacked(indices, ok):
+    """indices with every slot that points at a row without a valid block
+    (``ok`` False, see :func:`unpage`) replaced by -1."""
+    indices = indices.cpu().clone()
+    batch, length = ok.shape
+    inside = (indices >= 0) & (indices < length)
+    rows = indices.clamp(0, length - 1).long()
+    backed = torch.gather(ok[:, None, None, :].expand(-1, indices.shape[1], 1, -1), 3, rows)
+    indices[inside & ~backed] = -1
+    return indices
 
 
 def accuracy(actual, expected):

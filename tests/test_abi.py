@@ -22,7 +22,7 @@ def declared_functions():
 def test_header_declares_the_expected_entry_points():
     assert declared_functions() == sorted(
         ["dsa_version", "dsa_last_error", "dsa_plan_for", "dsa_plan_check", "dsa_partial_elems",
-         "dsa_fwd", "dsa_fwd_main", "dsa_merge"])
+         "dsa_fwd", "dsa_fwd_main", "dsa_fwd_opts", "dsa_fwd_main_opts", "dsa_merge"])
 
 
 def test_library_exports_every_declared_symbol():
@@ -40,6 +40,9 @@ def test_version_and_last_error():
 
 def test_struct_layout_matches_header():
     assert ctypes.sizeof(_lib.DsaPlan) == 32
+    # float, 3 x int32, pointer, 2 x int64
+    assert ctypes.sizeof(_lib.DsaFwdOptions) == 40
+    assert _lib.DsaFwdOptions.block_table.offset == 16
 
 
 def test_plan_for_rejects_bad_shapes():
@@ -83,3 +86,31 @@ def test_plan_check_accepts_valid(split):
     lib = _lib.load()
     plan = _lib.DsaPlan(64, 64, split, 2, 2, 32)
     assert lib.dsa_plan_check(ctypes.byref(plan), 1, 1, 128, 8192, 2048) == 0
+
+
+def _opts_call(lib, opts, L=1024):
+    """dsa_fwd_opts with fake (never dereferenced) 16-byte aligned pointers:
+    every case below must be rejected before any HIP call."""
+    fake = ctypes.c_void_p(1 << 20)
+    return lib.dsa_fwd_opts(fake, fake, fake, fake, fake, fake, fake, fake, None, None, None,
+                            1, 1, 16, L, 64, ctypes.byref(opts), None, None)
+
+
+def test_fwd_opts_validate_before_any_launch():
+    lib = _lib.load()
+    for bad in (-1.0, float("inf"), float("nan")):
+        assert _opts_call(lib, _lib.DsaFwdOptions(scale=bad)) < 0
+        assert b"scale" in lib.dsa_last_error()
+    table = ctypes.c_void_p(1 << 20)
+    # L must equal max_blocks * block_size
+    o = _lib.DsaFwdOptions(block_size=64, max_blocks=8, num_blocks=100, block_table=table)
+    assert _opts_call(lib, o, L=1000) < 0 and b"max_blocks" in lib.dsa_last_error()
+    # non-positive geometry
+    o = _lib.DsaFwdOptions(block_size=0, max_blocks=8, num_blocks=100, block_table=table)
+    assert _opts_call(lib, o, L=0 + 1024) < 0 and b"positive" in lib.dsa_last_error()
+    # pool too large for 32-bit row offsets
+    o = _lib.DsaFwdOptions(block_size=64, max_blocks=16, num_blocks=1 << 16, block_table=table)
+    assert _opts_call(lib, o, L=1024) < 0 and b"4194304" in lib.dsa_last_error()
+    # misaligned block table
+    o = _lib.DsaFwdOptions(block_size=64, max_blocks=16, num_blocks=100, block_table=ctypes.c_void_p((1 << 20) + 2))
+    assert _opts_call(lib, o, L=1024) < 0 and b"aligned" in lib.dsa_last_error()

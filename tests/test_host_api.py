@@ -146,3 +146,38 @@ def test_index_cache_limit_forces_split():
     with pytest.raises(ValueError):
         check_tuning(Tuning(64, 64, 2, kv_waves=2), (1, 1, 64, 100000, 8192))
     check_tuning(Tuning(64, 64, 4, kv_waves=2), (1, 1, 64, 100000, 8192))
+
+
+# ------------------------------------------------------- options beyond the reference
+@pytest.mark.parametrize("bad,exc", [("0.1", TypeError), (True, TypeError), (0.0, ValueError), (-0.5, ValueError),
+                                     (float("inf"), ValueError), (float("nan"), ValueError)])
+def test_scale_rejections(bad, exc):
+    with pytest.raises(exc):
+        dsa_amd.forward(*_tensors(), scale=bad)
+
+
+def _paged_tensors(B=2, SQ=3, H=16, blocks=9, bs=8, M=5, K=24, device="cpu"):
+    return (torch.zeros(B, SQ, H, 512, dtype=torch.bfloat16, device=device),
+            torch.zeros(blocks, bs, 1, 512, dtype=torch.bfloat16, device=device),
+            torch.zeros(B, SQ, H, 64, dtype=torch.bfloat16, device=device),
+            torch.zeros(blocks, bs, 1, 64, dtype=torch.bfloat16, device=device),
+            torch.zeros(B, SQ, 1, K, dtype=torch.int32, device=device),
+            torch.zeros(B, M, dtype=torch.int32, device=device))
+
+
+def test_paged_shape_contract():
+    q, kv, qr, kr, ids, table = _paged_tensors()
+    # the logical length is max_blocks * block_size; the pool shape is free
+    with pytest.raises(ValueError, match="ROCm GPU"):  # shapes pass; CPU tensors fail the device check
+        _check_inputs(q, kv, qr, kr, ids, table)
+    bad = {
+        "table rank": (q, kv, qr, kr, ids, table[0]),
+        "table batch": (q, kv, qr, kr, ids, torch.zeros(3, 5, dtype=torch.int32)),
+        "rope pool": (q, kv, qr, torch.zeros(9, 4, 1, 64, dtype=torch.bfloat16), ids, table),
+        "kv width": (q, torch.zeros(9, 8, 1, 256, dtype=torch.bfloat16), qr, kr, ids, table),
+    }
+    for name, args in bad.items():
+        with pytest.raises(ValueError):
+            _check_inputs(*args)
+        with pytest.raises(ValueError):
+            dsa_amd.forward(*args[:5], block_table=args[5])

@@ -229,3 +229,87 @@ def test_index_invariants():
     torch.testing.assert_close(o2, base[0], rtol=1e-5, atol=1e-6)
     torch.testing.assert_close(m2, base[1], rtol=0, atol=0)
     torch.testing.assert_close(s2, 2 * base[2], rtol=1e-6, atol=0)
+
+
+# ------------------------------------------------------- options beyond the reference
+@pytest.mark.parametrize("scale", [192 ** -0.5, 0.01])
+def test_scale_matches_library_sdpa(scale):
+    """``reference(scale=...)`` reduces to the library's attention at that scale."""
+    q, kv, qr, kr, ids = _small(11)
+    out, mx, sm = O.reference(q, kv, qr, kr, ids, scale=scale)
+    length = kv.shape[1]
+    for b in range(q.shape[0]):
+        for s in range(q.shape[1]):
+            idx = ids[b, s, 0].long()
+            valid = (idx >= 0) & (idx < length)
+            rows = kv[b, idx.clamp(0, length - 1), 0].double()
+            keys = torch.cat([rows, kr[b, idx.clamp(0, length - 1), 0].double()], dim=-1)
+            query = torch.cat([q[b, s].double(), qr[b, s].double()], dim=-1)
+            mask = valid[None, :].expand(q.shape[2], -1)
+            ref = torch.nn.functional.scaled_dot_product_attention(
+                query[None], keys[None], rows[None], attn_mask=mask[None], scale=scale)[0]
+            torch.testing.assert_close(out[b, s].double(), ref, rtol=2e-5, atol=2e-6)
+            score = (query @ keys.T) * scale
+            score[~mask] = -float("inf")
+            torch.testing.assert_close(mx[b, 0, s].double() + sm[b, 0, s].double().log(),
+                                       torch.logsumexp(score, -1), rtol=1e-6, atol=1e-6)
+
+
+def test_scale_default_is_the_reference_division():
+    data = _small(12)
+    for a, b in zip(O.reference(*data), O.reference(*data, scale=None)):
+        assert torch.equal(a.nan_to_num(), b.nan_to_num())
+
+
+def _paged(kv, kr, block_size, seed, holes=0):
+    """Pools holding kv / k_rope under a random block permutation (plus spare
+    blocks), the block table, and optionally `holes` entries set to -1."""
+    g = torch.Generator().manual_seed(seed)
+    batch, length = kv.shape[:2]
+    per = length // block_size
+    blocks = batch * per + 3
+    order = torch.randperm(blocks, generator=g)[: batch * per].view(batch, per)
+    kv_pool = torch.randn(blocks, block_size, 1, 512, generator=g).bfloat16()
+    kr_pool = torch.randn(blocks, block_size, 1, 64, generator=g).bfloat16()
+    for b in range(batch):
+        for m in range(per):
+            kv_pool[order[b, m]] = kv[b, m * block_size:(m + 1) * block_size]
+            kr_pool[order[b, m]] = kr[b, m * block_size:(m + 1) * block_size]
+    table = order.int().contiguous()
+    if holes:
+        flat = table.view(-1)
+        flat[torch.randperm(flat.numel(), generator=g)[:holes]] = -1
+    return kv_pool, kr_pool, table
+
+
+def test_unpage_identity_and_permuted_tables():
+    q, kv, qr, kr, ids = _small(13, length=96)
+    # identity table: pool = kv split into consecutive blocks
+    pool, rpool = kv.reshape(2 * 6, 16, 1, 512), kr.reshape(2 * 6, 16, 1, 64)
+    table = torch.arange(12, dtype=torch.int32).view(2, 6)
+    ukv, ukr, ok = O.unpage(pool, rpool, table)
+    assert torch.equal(ukv, kv) and torch.equal(ukr, kr) and bool(ok.all())
+    # permuted table with spare blocks reproduces kv exactly
+    kv_pool, kr_pool, table = _paged(kv, kr, 16, seed=1)
+    ukv, ukr, ok = O.unpage(kv_pool, kr_pool, table)
+    assert torch.equal(ukv, kv) and torch.equal(ukr, kr) and bool(ok.all())
+
+
+def test_unpage_matches_elementwise_gather_and_masks_holes():
+    q, kv, qr, kr, ids = _small(14, length=96)
+    kv_pool, kr_pool, table = _paged(kv, kr, 32, seed=2, holes=2)
+    ukv, ukr, ok = O.unpage(kv_pool, kr_pool, table)
+    for b in range(2):
+        for i in range(96):
+            blk = int(table[b, i // 32])
+            assert bool(ok[b, i]) == (0 <= blk < kv_pool.shape[0])
+            if ok[b, i]:
+                assert torch.equal(ukv[b, i], kv_pool[blk, i % 32])
+                assert torch.equal(ukr[b, i], kr_pool[blk, i % 32])
+    masked = O.mask_unbacked(ids, ok)
+    for b in range(2):
+        for s in range(ids.shape[1]):
+            for j in range(ids.shape[-1]):
+                v = int(ids[b, s, 0, j])
+                hole = 0 <= v < 96 and not bool(ok[b, v])
+                assert int(masked[b, s, 0, j]) == (-1 if hole else v)
