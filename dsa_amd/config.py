@@ -99,29 +99,28 @@ def check_tuning(config: Tuning, shape) -> None:
     _lib.check(_lib.load().dsa_plan_check(ctypes.byref(plan), b, sq, h, length, topk), "invalid Tuning")
 
 
-# Per-shape plans for MI355X (256 CUs), re-derived from the reference's table
-# (dsa/config.py:42-59) for gfx950: four waves per workgroup, one 152 KiB
-# workgroup per CU, 32-head waves wherever H is a multiple of 64 (128-head
-# workgroups when H is a multiple of 128), KV split until the grid covers the
-# CUs.
+# Per-shape plans for MI355X (256 CUs), the counterpart of the reference's
+# table (dsa/config.py:42-59): the library planner's choice (dsa_plan_for, a
+# cost model fitted to MI355X measurements), except where a measured sweep
+# found a faster plan (decode_b32, prefill_q16, prefill_q64, decode_b4_h128).
 SELECTED = {
-    "decode_b1": Tuning(128, 32, 64, stages=4),
+    "decode_b1": Tuning(16, 64, 16, kv_waves=4, mfma=16),
     "decode_b8": Tuning(32, 64, 8, kv_waves=2, mfma=16),
-    "decode_b32": Tuning(128, 32, 8, stages=4),
-    "decode_tp8": Tuning(16, 64, 32, kv_waves=4, mfma=16),
-    "prefill_q16": Tuning(128, 32, 16, stages=4),
-    "prefill_q64": Tuning(128, 32, 4, stages=4),
+    "decode_b32": Tuning(32, 64, 2, kv_waves=2, mfma=16),
+    "decode_tp8": Tuning(16, 64, 16, kv_waves=4, mfma=16),
+    "prefill_q16": Tuning(32, 64, 4, kv_waves=2, mfma=16),
+    "prefill_q64": Tuning(32, 64, 1, kv_waves=2, mfma=16),
     "prefill_tp8": Tuning(16, 64, 2, kv_waves=4, mfma=16),
-    "prefill_k512": Tuning(64, 64, 2, kv_waves=2),
-    "decode_b4_h128": Tuning(128, 32, 64, stages=4),
+    "prefill_k512": Tuning(32, 64, 1, kv_waves=2, mfma=16),
+    "decode_b4_h128": Tuning(16, 64, 8, kv_waves=4, mfma=16),
     "prefill_b4_h128": Tuning(128, 32, 1, stages=4),
-    "decode_b4_h64": Tuning(64, 64, 32, kv_waves=2),
+    "decode_b4_h64": Tuning(16, 64, 16, kv_waves=4, mfma=16),
     "prefill_b4_h64": Tuning(64, 64, 1, kv_waves=2),
-    "decode_b4_h32": Tuning(32, 64, 32, kv_waves=2, mfma=16),
+    "decode_b4_h32": Tuning(16, 64, 16, kv_waves=4, mfma=16),
     "prefill_b4_h32": Tuning(32, 64, 1, kv_waves=2, mfma=16),
-    "decode_b4_h16": Tuning(16, 64, 32, kv_waves=4, mfma=16),
+    "decode_b4_h16": Tuning(16, 64, 16, kv_waves=4, mfma=16),
     "prefill_b4_h16": Tuning(16, 64, 1, kv_waves=4, mfma=16),
-    "c1_decode_b1": Tuning(128, 32, 64, stages=4),
+    "c1_decode_b1": Tuning(16, 64, 16, kv_waves=4, mfma=16),
     "c2_decode_b8": Tuning(32, 64, 8, kv_waves=2, mfma=16),
     "c3_decode_h16_mtp": Tuning(16, 64, 2, kv_waves=4, mfma=16),
     "c4_prefill_h16": Tuning(16, 64, 1, kv_waves=4, mfma=16),

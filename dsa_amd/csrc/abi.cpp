@@ -79,31 +79,64 @@ int dsa_plan_for(int B, int SQ, int H, int L, int TOPK, int num_cus, dsa_plan* o
     if (!out) return fail(-1, "out is NULL");
     if (int rc = check_shape(B, SQ, H, L, TOPK)) return rc;
     if (num_cus <= 0) return fail(-1, "num_cus must be positive (got %d)", num_cus);
-    dsa_plan p{};
-    // Four waves per workgroup.  Head counts that are multiples of 64 use the
-    // 32x32x16 MFMA variant (32 heads per wave): 128 heads x 1 row stream on
-    // 32-row tiles with a 4-stage ring, or 64 heads x 2 row streams on 64-row
-    // tiles; other head counts use the 16x16x32 variant: 32 x 2 or 16 x 4.
+    // Every (variant, split) the kernels support is scored with a cost model
+    // fitted to MI355X measurements, and the cheapest is taken.  One
+    // workgroup (152 KiB of LDS) runs per CU, so workgroups beyond the CU
+    // count run in further rounds.  Per workgroup: a prologue (index load,
+    // first gather), a cost per tile, and an epilogue (row-wave merge and
+    // partial stores); the gathered rows are also bounded by the HBM rate the
+    // active CUs reach; a split adds the merge kernel, bounded by its
+    // parallelism.
+    struct Variant {
+        int hpg, kvw, bn, stages, mfma;
+        double tile_cycles, epilogue_cycles;
+    };
+    static const Variant kVariants[] = {
+        {128, 1, 32, 4, 32, 4400.0, 18000.0},  // wide<4,1,32,4>
+        {64, 2, 64, 2, 32, 5000.0, 15000.0},   // wide<2,2,64,2>
+        {64, 1, 64, 2, 16, 7000.0, 6000.0},    // narrow<4,1>
+        {32, 2, 64, 2, 16, 4000.0, 10000.0},   // narrow<2,2>
+        {16, 4, 64, 2, 16, 2800.0, 10000.0},   // narrow<1,4>
+    };
+    constexpr double kClockMHz = 2200.0, kPrologueCycles = 9000.0, kLaunchUs = 2.0;
+    constexpr double kHbmBytesPerUs = 4.8e6, kCuBytesPerUs = 3.0e4;                // sustained gather rates
+    constexpr double kMergeUs = 2.0, kMergeWgBytesPerUs = 4.2e4, kMergeBytesPerUs = 6.0e6;
     const int64_t tokens = (int64_t)B * SQ;
-    if (H % 128 == 0) {
-        p.heads_per_group = 128, p.kv_waves = 1, p.mfma = 32, p.tile_rows = 32, p.stages = 4;
-    } else if (H % 64 == 0) {
-        p.heads_per_group = 64, p.kv_waves = 2, p.mfma = 32, p.tile_rows = 64, p.stages = 2;
-    } else if (H % 32 == 0) {
-        p.heads_per_group = 32, p.kv_waves = 2, p.mfma = 16, p.tile_rows = 64, p.stages = 2;
-    } else {
-        p.heads_per_group = 16, p.kv_waves = 4, p.mfma = 16, p.tile_rows = 64, p.stages = 2;
+    const double gathered = (double)tokens * TOPK * 1152.0;
+    double best = -1.0;
+    dsa_plan p{};
+    for (const Variant& v : kVariants) {
+        if (H % v.hpg) continue;
+        const int ntiles = ceil_div(TOPK, v.bn);
+        const int min_split = ceil_div(ntiles * v.bn, DSA_IDX_CAP);
+        const int64_t groups = tokens * (H / v.hpg);
+        for (int split = min_split; split <= ntiles; ++split) {
+            const int64_t wgs = groups * split;
+            if (wgs > 0x7fffffff) break;
+            const double rounds = (double)((wgs + num_cus - 1) / num_cus);
+            const double tiles = (double)ceil_div(ntiles, split);
+            const double wg_us = (kPrologueCycles + tiles * v.tile_cycles + v.epilogue_cycles) / kClockMHz;
+            const double active = (double)(wgs < num_cus ? wgs : num_cus);
+            const double hbm = active * kCuBytesPerUs < kHbmBytesPerUs ? active * kCuBytesPerUs : kHbmBytesPerUs;
+            double main_us = rounds * wg_us;
+            if (gathered / hbm > main_us) main_us = gathered / hbm;
+            double merge_us = 0.0;
+            if (split > 1) {
+                const double bytes = (double)tokens * split * H * 2056.0;
+                const double merge_wgs = (double)tokens * ((H + 1) / 2);
+                const double bw = merge_wgs * kMergeWgBytesPerUs < kMergeBytesPerUs ? merge_wgs * kMergeWgBytesPerUs
+                                                                                    : kMergeBytesPerUs;
+                merge_us = kMergeUs + bytes / bw;
+            }
+            const double cost = kLaunchUs + main_us + merge_us;
+            if (best < 0.0 || cost < best * 0.999) {
+                best = cost;
+                p.heads_per_group = v.hpg, p.kv_waves = v.kvw, p.tile_rows = v.bn, p.stages = v.stages;
+                p.mfma = v.mfma, p.split = split;
+            }
+        }
     }
-    // One 152 KiB workgroup fits a CU; split the KV range until the grid covers
-    // every CU once, but never below one tile per split.
-    const int ntiles = ceil_div(TOPK, p.tile_rows);
-    const int64_t base = tokens * (H / p.heads_per_group);
-    int split = 1;
-    if (base < num_cus) split = (int)((num_cus + base - 1) / base);
-    if (split > ntiles) split = ntiles;
-    const int min_split = ceil_div(ntiles * p.tile_rows, DSA_IDX_CAP);
-    if (split < min_split) split = min_split;
-    p.split = split;
+    if (best < 0.0) return fail(-1, "no kernel variant for H=%d", H);
     *out = p;
     return dsa_plan_check(out, B, SQ, H, L, TOPK);
 }
