@@ -69,10 +69,16 @@ def algorithmic_units(shape):
 class Call:
     """One preallocated forward call through the C ABI."""
 
-    def __init__(self, data, config: Tuning):
+    def __init__(self, data, config: Tuning, block_table=None):
         self.data = data
         q = data[0]
-        self.shape = tuple(q.shape[:3]) + (data[1].shape[1], data[4].shape[-1])
+        length = data[1].shape[1] if block_table is None else block_table.shape[1] * data[1].shape[1]
+        self.shape = tuple(q.shape[:3]) + (length, data[4].shape[-1])
+        self.opts = None
+        if block_table is not None:  # paged kv: data[1], data[3] are block pools
+            self.block_table = block_table
+            self.opts = _lib.DsaFwdOptions(block_size=data[1].shape[1], max_blocks=block_table.shape[1],
+                                           num_blocks=data[1].shape[0], block_table=block_table.data_ptr())
         b, sq, h, _, _ = self.shape
         self.config = config
         self.plan = config.to_c()
@@ -92,7 +98,11 @@ class Call:
 
     def main(self, stream):
         b, sq, h, length, k = self.shape
-        rc = self.lib.dsa_fwd_main(*self.args, b, sq, h, length, k, ctypes.byref(self.plan), stream)
+        if self.opts is None:
+            rc = self.lib.dsa_fwd_main(*self.args, b, sq, h, length, k, ctypes.byref(self.plan), stream)
+        else:
+            rc = self.lib.dsa_fwd_main_opts(*self.args, b, sq, h, length, k, ctypes.byref(self.opts),
+                                            ctypes.byref(self.plan), stream)
         if rc:
             _lib.check(rc, "dsa_fwd_main")
 
@@ -182,6 +192,23 @@ def traffic_from_profiles(name):
     return json.loads(path.read_text()).get("hbm_bytes_per_launch")
 
 
+def paged(data, block_size, seed):
+    """The same logical inputs with kv / k_rope moved into block pools under a
+    random block permutation: (data with pools, block table)."""
+    q, kv, qr, kr, ids = data
+    batch, length = kv.shape[:2]
+    if length % block_size:
+        raise SystemExit(f"--paged {block_size} must divide L={length}")
+    per = length // block_size
+    g = torch.Generator(device=kv.device).manual_seed(seed)
+    perm = torch.randperm(batch * per, device=kv.device, generator=g)
+    kv_pool = torch.empty((batch * per, block_size, 1, 512), device=kv.device, dtype=kv.dtype)
+    kr_pool = torch.empty((batch * per, block_size, 1, 64), device=kv.device, dtype=kv.dtype)
+    kv_pool[perm] = kv.view(batch * per, block_size, 1, 512)
+    kr_pool[perm] = kr.view(batch * per, block_size, 1, 64)
+    return (q, kv_pool, qr, kr_pool, ids), perm.view(batch, per).int().contiguous()
+
+
 def run(name, args):
     shape = BASELINE_CONFIGS[name]
     rotate = args.rotate if args.rotate else DEFAULT_ROTATE[name]
@@ -193,7 +220,15 @@ def run(name, args):
         config = Tuning(bm, bn, split, kv_waves=kv_waves, stages=stages, mfma=mfma)
     print(f"[bench] {name} shape={shape} plan={config} rotate={rotate}", file=sys.stderr, flush=True)
     sets = [baseline_inputs(name, seed=args.seed + i, device="cuda", cpu_recipe=False) for i in range(rotate)]
-    calls = [Call(d, config) for d in sets]
+    if args.paged:
+        calls = []
+        for i, d in enumerate(sets):
+            pd, table = paged(d, args.paged, args.seed + i)
+            calls.append(Call(pd, config, block_table=table))
+            if i:  # set 0 stays for the CPU baseline
+                sets[i] = None
+    else:
+        calls = [Call(d, config) for d in sets]
     wall, main_us, merge_us, span_us = time_calls(calls, args.steps, args.warmup)
     _, warm_main, _, warm_span = time_calls(calls[:1], args.steps, args.warmup)
     gbytes, flops = algorithmic_units(shape)
@@ -215,10 +250,11 @@ def run(name, args):
         "vs_baseline": (round(span_us / PUBLISHED_SPAN_US[name], 4) if name in PUBLISHED_SPAN_US else None),
         "dtype": "bf16",
         "data": (f"synthetic: seeded N(0,1) bf16 q/kv/rope, per-workload index recipe, "
-                 f"{rotate} rotating input set(s) resident in HBM"),
+                 f"{rotate} rotating input set(s) resident in HBM"
+                 + (f"; kv paged in {args.paged}-row blocks under a random block table" if args.paged else "")),
         "config": {"workload": name, "B": shape[0], "SQ": shape[1], "H": shape[2], "L": shape[3],
                    "TOPK": shape[4], "plan": vars(config) if hasattr(config, "__dict__") else str(config),
-                   "rotating_input_sets": rotate},
+                   "rotating_input_sets": rotate, "paged_block_size": args.paged or None},
         "roofline": {"bound": bound, "achieved": round(achieved, 2), "peak": peak, "unit": unit,
                      "frac": round(achieved / peak, 4), "traffic": traffic_from_profiles(name),
                      "kernel": f"sparse_mla_fwd (main), {gbytes} gathered B and {flops} FLOP per launch"},
@@ -249,6 +285,8 @@ def main():
     ap.add_argument("--rotate", type=int, default=0, help="input sets to cycle (default per workload)")
     ap.add_argument("--plan", default="", help="override the plan: bm,split,kv_waves,mfma[,bn,stages]")
     ap.add_argument("--seed", type=int, default=20261102)
+    ap.add_argument("--paged", type=int, default=0, metavar="BLOCK",
+                    help="run the workload on paged kv (block pools of BLOCK rows, random block table)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU oracle timing")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",

@@ -38,8 +38,8 @@ int check_shape(int B, int SQ, int H, int L, int TOPK) {
     if (B <= 0 || SQ <= 0 || H <= 0 || L <= 0 || TOPK <= 0)
         return fail(-1, "all of B, SQ, H, L, TOPK must be positive (got %d, %d, %d, %d, %d)", B, SQ, H, L, TOPK);
     if (H % 16 != 0) return fail(-1, "H must be a multiple of 16 (got %d)", H);
-    // kv rows of one batch are addressed with 32-bit byte offsets
-    if (L >= (1 << 22)) return fail(-1, "L must be below 4194304 (got %d)", L);
+    // k_rope rows of one batch are addressed with 32-bit byte offsets
+    if (L >= (1 << 25)) return fail(-1, "L must be below 33554432 (got %d)", L);
     if ((int64_t)B * SQ > (int64_t)1 << 30) return fail(-1, "B*SQ too large");
     return 0;
 }
@@ -195,8 +195,8 @@ int fwd_impl(const uint16_t* q, const uint16_t* kv, const uint16_t* q_rope, cons
                             block_size, max_blocks, opts->num_blocks);
             if ((int64_t)max_blocks * block_size != L)
                 return fail(-1, "L must equal max_blocks * block_size (%d != %d * %d)", L, max_blocks, block_size);
-            if ((int64_t)opts->num_blocks * block_size >= (1 << 22))
-                return fail(-1, "num_blocks * block_size must be below 4194304 (got %lld)",
+            if ((int64_t)opts->num_blocks * block_size >= (1 << 25))
+                return fail(-1, "num_blocks * block_size must be below 33554432 (got %lld)",
                             (long long)opts->num_blocks * block_size);
             if ((uintptr_t)block_table & 3) return fail(-1, "block_table must be 4-byte aligned");
             kv_rows = opts->num_blocks * block_size;

@@ -111,21 +111,31 @@ __device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
 // Gathers write LDS with buffer_load_dwordx4 ... lds: lane l's 16 bytes land
 // at m0 + 16*l.  They are issued as inline asm so the compiler does not
 // serialise later LDS reads behind them; completion is tracked with
-// Ring::wait_tile().  m0 and the buffer offsets are wave-uniform by construction.
+// Ring::wait_tile().  m0 and the buffer descriptors are wave-uniform by
+// construction.
 //
-// One kv row: lane l loads bytes row_off + ((16*l) ^ xor16) of the buffer.
-// The XOR is part of the asm so no per-row lane offset is ever kept live.
-__device__ __forceinline__ void gather_row(uint32_t lds_base, rsrc_t rsrc, uint32_t row_off, uint32_t lane16,
-                                           uint32_t xor16) {
+// One kv row: a 1 KiB descriptor at the row's 64-bit address (so the kv
+// pool has no 4 GiB limit), lane l loading bytes (16*l) ^ xor16 of it.  The
+// XOR is part of the asm so no per-row lane offset is ever kept live.
+__device__ __forceinline__ rsrc_t row_rsrc(const char* base, uint32_t row) {
+    const uint64_t a = reinterpret_cast<uint64_t>(base) + ((uint64_t)row << 10);
+    rsrc_t r;
+    r[0] = (int)(uint32_t)a;
+    r[1] = (int)((a >> 32) & 0xffff);
+    r[2] = 1024;
+    r[3] = 0x00020000;
+    return r;
+}
+__device__ __forceinline__ void gather_row(uint32_t lds_base, rsrc_t rsrc, uint32_t lane16, uint32_t xor16) {
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
     uint32_t voff;
     asm volatile(
         "v_xor_b32 %0, %1, %2\n\t"
         "s_mov_b32 m0, %3\n\t"
-        "buffer_load_dwordx4 %0, %4, %5 offen lds"
+        "buffer_load_dwordx4 %0, %4, 0 offen lds"
         : "=&v"(voff)
-        : "s"(xor16), "v"(lane16), "s"(__builtin_amdgcn_readfirstlane(lds_base)), "s"(rsrc), "s"(row_off)
+        : "s"(xor16), "v"(lane16), "s"(__builtin_amdgcn_readfirstlane(lds_base)), "s"(rsrc)
         : "memory", "m0");
 #pragma clang diagnostic pop
 }
@@ -313,12 +323,13 @@ __device__ __forceinline__ void store_indices(const IdxRegs& r, uint32_t idx_lds
 
 // Buffer resources over this workgroup's batch of kv and k_rope.
 struct Gather {
-    rsrc_t kv, kr;
+    const char* kv;  // first kv row of the addressed range
+    rsrc_t kr;       // k_rope rows of the range (32-bit per-lane offsets: < 2^25 rows)
 };
 __device__ __forceinline__ Gather make_gather(const FwdParams& p, int b) {
     const int64_t rows = p.block_table ? 0 : (int64_t)b * p.L;  // first row of the addressed range
     Gather g;
-    g.kv = make_rsrc(reinterpret_cast<const char*>(p.kv) + rows * 1024, (uint32_t)p.kv_rows * 1024u);
+    g.kv = reinterpret_cast<const char*>(p.kv) + rows * 1024;
     g.kr = make_rsrc(reinterpret_cast<const char*>(p.k_rope) + rows * 128, (uint32_t)p.kv_rows * 128u);
     return g;
 }
@@ -333,13 +344,13 @@ __device__ __forceinline__ void issue_tile(const FwdParams& p, const Gather& gt,
     const int rows = p.kv_rows;
     const int r0 = wave * R::KV_PER_WAVE;
     const int my_id = lds_load<int>(idx_lds + 4 * (t * R::BN + r0 + (lane % R::KV_PER_WAVE)));
-    const uint32_t my_off = (uint32_t)min(max(my_id, 0), rows - 1) << 10;
+    const uint32_t my_row = (uint32_t)min(max(my_id, 0), rows - 1);
     const uint32_t lane16 = (uint32_t)lane << 4;
 #pragma unroll
     for (int rr = 0; rr < R::KV_PER_WAVE; ++rr) {
         const int r = r0 + rr;
-        const uint32_t row_off = __builtin_amdgcn_readlane(my_off, rr);
-        gather_row(stage + r * 1024, gt.kv, row_off, lane16, (uint32_t)sw_kv(r) << 4);
+        gather_row(stage + r * 1024, row_rsrc(gt.kv, __builtin_amdgcn_readlane(my_row, rr)), lane16,
+                   (uint32_t)sw_kv(r) << 4);
     }
 #pragma unroll
     for (int jj = 0; jj < R::ROPE_PER_WAVE; ++jj) {

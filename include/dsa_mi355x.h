@@ -144,7 +144,7 @@ int dsa_fwd_main(const uint16_t* q, const uint16_t* kv, const uint16_t* q_rope,
  *                 row I of batch b is pool row
  *                 block_table[b * max_blocks + I / block_size] * block_size
  *                 + I % block_size.  L must equal max_blocks * block_size and
- *                 num_blocks * block_size must be below 4194304.  Indices stay
+ *                 num_blocks * block_size must be below 33554432.  Indices stay
  *                 logical and are masked as in dsa_fwd; a slot whose block
  *                 entry lies outside [0, num_blocks) is masked as well.
  */

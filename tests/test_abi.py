@@ -109,8 +109,8 @@ def test_fwd_opts_validate_before_any_launch():
     o = _lib.DsaFwdOptions(block_size=0, max_blocks=8, num_blocks=100, block_table=table)
     assert _opts_call(lib, o, L=0 + 1024) < 0 and b"positive" in lib.dsa_last_error()
     # pool too large for 32-bit row offsets
-    o = _lib.DsaFwdOptions(block_size=64, max_blocks=16, num_blocks=1 << 16, block_table=table)
-    assert _opts_call(lib, o, L=1024) < 0 and b"4194304" in lib.dsa_last_error()
+    o = _lib.DsaFwdOptions(block_size=64, max_blocks=16, num_blocks=1 << 19, block_table=table)
+    assert _opts_call(lib, o, L=1024) < 0 and b"33554432" in lib.dsa_last_error()
     # misaligned block table
     o = _lib.DsaFwdOptions(block_size=64, max_blocks=16, num_blocks=100, block_table=ctypes.c_void_p((1 << 20) + 2))
     assert _opts_call(lib, o, L=1024) < 0 and b"aligned" in lib.dsa_last_error()
