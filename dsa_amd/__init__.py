@@ -2,9 +2,13 @@
 
 Public surface mirrors the reference package (dsa/__init__.py:2-5):
 ``forward``, ``Tuning``, ``CASE_SHAPES``, ``SELECTED``; plus ``merge`` (the
-standalone FP32 split merge) and ``select`` (the plan for a shape).
+standalone FP32 split merge), ``select`` (the plan for a shape) and the
+lightning indexer that produces the indices (``indexer``, ``indexer_logits``,
+``indexer_topk``).
 """
 from .api import forward, merge, plan_call
 from .config import CASE_SHAPES, SELECTED, Tuning, select
+from .indexer import indexer, indexer_logits, indexer_topk
 
-__all__ = ["forward", "merge", "plan_call", "Tuning", "CASE_SHAPES", "SELECTED", "select"]
+__all__ = ["forward", "merge", "plan_call", "Tuning", "CASE_SHAPES", "SELECTED", "select",
+           "indexer", "indexer_logits", "indexer_topk"]

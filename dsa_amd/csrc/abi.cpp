@@ -300,3 +300,54 @@ int dsa_fwd_main_opts(const uint16_t* q, const uint16_t* kv, const uint16_t* q_r
 }
 
 }  // extern "C"
+
+extern "C" {
+
+int dsa_indexer_logits(const uint16_t* q_idx, const uint16_t* k_idx, const float* weights, const int32_t* lengths,
+                       float* logits, int B, int SQ, int HI, int L, hipStream_t stream) {
+    if (!q_idx || !k_idx || !weights || !lengths || !logits) return fail(-1, "NULL pointer argument");
+    if (B <= 0 || SQ <= 0 || L <= 0) return fail(-1, "B, SQ, L must be positive (got %d, %d, %d)", B, SQ, L);
+    if (HI != 32 && HI != 64) return fail(-1, "indexer heads must be 32 or 64 (got %d)", HI);
+    // keys of one batch are addressed with 32-bit byte offsets
+    if (L >= (1 << 24)) return fail(-1, "L must be below 16777216 (got %d)", L);
+    if (((uintptr_t)q_idx | (uintptr_t)k_idx) & 15) return fail(-1, "q_idx and k_idx must be 16-byte aligned");
+    if (((uintptr_t)weights | (uintptr_t)lengths | (uintptr_t)logits) & 3)
+        return fail(-1, "weights, lengths and logits must be 4-byte aligned");
+    dsa::IndexerParams p{};
+    p.q = q_idx;
+    p.k = k_idx;
+    p.w = weights;
+    p.len = lengths;
+    p.logits = logits;
+    p.B = B;
+    p.SQ = SQ;
+    p.HI = HI;
+    p.L = L;
+    p.tgroups = ceil_div(SQ, 256 / HI);
+    p.ntiles = ceil_div(L, 64);
+    // About 1024 workgroups: decode spreads one query's keys over many CUs,
+    // prefill keeps every key tile of a query group in one workgroup.
+    const int64_t work = (int64_t)B * p.tgroups * p.ntiles;
+    p.tiles_per_wg = (int)((work + 1023) / 1024);
+    if (p.tiles_per_wg < 1) p.tiles_per_wg = 1;
+    if (p.tiles_per_wg > p.ntiles) p.tiles_per_wg = p.ntiles;
+    if ((int64_t)B * p.tgroups > 0x7fffffff) return fail(-1, "grid too large");
+    const int rc = dsa::launch_indexer_logits(p, stream);
+    if (rc) return hip_fail(rc, "indexer logits launch");
+    g_err[0] = 0;
+    return 0;
+}
+
+int dsa_indexer_topk(const float* logits, const int32_t* lengths, int32_t* indices, int B, int SQ, int L, int TOPK,
+                     hipStream_t stream) {
+    if (!logits || !lengths || !indices) return fail(-1, "NULL pointer argument");
+    if (B <= 0 || SQ <= 0 || L <= 0 || TOPK <= 0)
+        return fail(-1, "B, SQ, L, TOPK must be positive (got %d, %d, %d, %d)", B, SQ, L, TOPK);
+    if ((int64_t)B * SQ > 0x7fffffff) return fail(-1, "too many rows");
+    const int rc = dsa::launch_indexer_topk(logits, lengths, indices, B * SQ, L, TOPK, stream);
+    if (rc) return hip_fail(rc, "indexer top-k launch");
+    g_err[0] = 0;
+    return 0;
+}
+
+}  // extern "C"

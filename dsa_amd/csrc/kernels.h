@@ -52,3 +52,28 @@ int launch_merge(const float* part_o, const float* part_m, const float* part_l,
                  int tokens, int H, int nsplit, hipStream_t stream);
 
 }  // namespace dsa
+
+namespace dsa {
+
+// Lightning indexer (the token selector in front of the sparse attention).
+struct IndexerParams {
+    const uint16_t* q;       // [B, SQ, HI, 128] bf16 indexer queries
+    const uint16_t* k;       // [B, L, 128] bf16 indexer keys
+    const float* w;          // [B, SQ, HI] head weights
+    const int32_t* len;      // [B, SQ] candidate keys per query (keys [0, len) are candidates)
+    float* logits;           // [B, SQ, L] fp32; defined for s < len
+    int B, SQ, HI, L;
+    int tgroups;             // query groups per batch: ceil(SQ / (256 / HI))
+    int ntiles;              // ceil(L / 64) key tiles
+    int tiles_per_wg;        // key tiles per workgroup
+};
+
+// Enqueue the logits kernel (HI = 32 or 64); returns a hipError_t.
+int launch_indexer_logits(const IndexerParams& p, hipStream_t stream);
+
+// Enqueue the top-k selection: per row, the TOPK keys of largest logit among
+// s < len (ties: lower s first), written in ascending s order, -1 padded.
+int launch_indexer_topk(const float* logits, const int32_t* len, int32_t* indices, int rows, int L, int topk,
+                        hipStream_t stream);
+
+}  // namespace dsa

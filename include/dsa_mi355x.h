@@ -187,6 +187,30 @@ int dsa_merge(const float* part_o, const float* part_m, const float* part_l,
               uint16_t* out, float* out_max, float* out_sum,
               int tokens, int H, int split, hipStream_t stream);
 
+/*
+ * Lightning indexer: the token selector that produces `idx` for dsa_fwd (the
+ * step before the attention; no reference counterpart -- the reference takes
+ * the indices as an input, README.md:19-21).
+ *
+ *   logits[t, s] = sum_j w[t, j] * relu(q_idx[t, j, :] . k_idx[b, s, :])   for s < len[t]
+ *
+ *   q_idx   [B, SQ, HI, 128] bf16 (HI = 32 or 64)   k_idx [B, L, 128] bf16
+ *   weights [B, SQ, HI] fp32                        lengths [B, SQ] int32, clamped to [0, L]
+ *   logits  [B, SQ, L] fp32: defined for s < lengths[t] (entries past a row's
+ *           length are unspecified).
+ *
+ * dsa_indexer_topk: for every row, the TOPK keys s < lengths[t] of largest
+ * logit (ties: lower s first), written to indices [B, SQ, 1, TOPK] in
+ * ascending s order and padded with -1 -- directly the `idx` of dsa_fwd.
+ * Bit-exact given the same logits.
+ */
+int dsa_indexer_logits(const uint16_t* q_idx, const uint16_t* k_idx, const float* weights,
+                       const int32_t* lengths, float* logits,
+                       int B, int SQ, int HI, int L, hipStream_t stream);
+
+int dsa_indexer_topk(const float* logits, const int32_t* lengths, int32_t* indices,
+                     int B, int SQ, int L, int TOPK, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

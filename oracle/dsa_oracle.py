@@ -25,6 +25,10 @@ Functions and the reference code each one restates:
                          reference takes contiguous kv only), so paged runs are
                          checked against the same ``reference``.
 
+* ``indexer_logits_ref`` / ``indexer_topk_ref`` / ``float_key`` -- the
+                         lightning indexer (no reference counterpart: the
+                         reference takes the indices as an input).
+
 ``reference(scale=...)`` generalises the fixed 1/24 (tools/review.py:140) to
 another softmax scale; the default keeps the reference's exact division.
 
@@ -117,6 +121,50 @@ def mask_unbacked(indices, ok):
     backed = torch.gather(ok[:, None, None, :].expand(-1, indices.shape[1], 1, -1), 3, rows)
     indices[inside & ~backed] = -1
     return indices
+
+
+def indexer_logits_ref(q_idx, k_idx, weights, lengths, chunk: int = 64):
+    """FP32 lightning-indexer logits ``[B, SQ, L]``:
+    ``sum_j w[t, j] * relu(q_idx[t, j] . k_idx[s])`` for ``s < lengths[t]``,
+    -inf beyond (no reference counterpart; the DSA indexer's definition)."""
+    q, k, w, lengths = (t.cpu() for t in (q_idx, k_idx, weights, lengths))
+    batch, queries, _, _ = q.shape
+    length = k.shape[1]
+    out = torch.empty((batch, queries, length))
+    for b in range(batch):
+        kb = k[b].float()
+        for t0 in range(0, queries, chunk):
+            qs = q[b, t0:t0 + chunk].float()                      # [c, HI, 128]
+            dots = torch.einsum("chd,sd->chs", qs, kb)            # [c, HI, L]
+            out[b, t0:t0 + chunk] = (dots.clamp_min(0) * w[b, t0:t0 + chunk].float()[..., None]).sum(1)
+    cols = torch.arange(length)
+    out.masked_fill_(cols[None, None, :] >= lengths.clamp(0, length)[..., None].long(), -float("inf"))
+    return out
+
+
+def float_key(values):
+    """Order-preserving uint32 keys of float32 values (larger value, larger
+    key; -0.0 below +0.0), the order the device selection uses."""
+    bits = np.ascontiguousarray(np.asarray(values, dtype=np.float32)).view(np.uint32)
+    return np.where(bits & np.uint32(0x80000000), ~bits, bits | np.uint32(0x80000000)).astype(np.uint32)
+
+
+def indexer_topk_ref(logits, lengths, topk: int):
+    """``indices [B, SQ, 1, topk]`` int32: per row the ``topk`` largest logits
+    among ``s < lengths`` by :func:`float_key` (ties: lower s first), in
+    ascending s order, padded with -1."""
+    logits = logits.cpu().float().numpy()
+    lengths = lengths.cpu().numpy()
+    batch, queries, length = logits.shape
+    out = np.full((batch, queries, 1, topk), -1, dtype=np.int32)
+    for b in range(batch):
+        for t in range(queries):
+            n = int(min(max(lengths[b, t], 0), length))
+            keys = float_key(logits[b, t, :n])
+            order = np.lexsort((np.arange(n), ~keys))  # key descending, then s ascending
+            chosen = np.sort(order[:topk])
+            out[b, t, 0, :chosen.size] = chosen
+    return torch.from_numpy(out)
 
 
 def accuracy(actual, expected):

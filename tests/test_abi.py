@@ -22,7 +22,8 @@ def declared_functions():
 def test_header_declares_the_expected_entry_points():
     assert declared_functions() == sorted(
         ["dsa_version", "dsa_last_error", "dsa_plan_for", "dsa_plan_check", "dsa_partial_elems",
-         "dsa_fwd", "dsa_fwd_main", "dsa_fwd_opts", "dsa_fwd_main_opts", "dsa_merge"])
+         "dsa_fwd", "dsa_fwd_main", "dsa_fwd_opts", "dsa_fwd_main_opts", "dsa_merge",
+         "dsa_indexer_logits", "dsa_indexer_topk"])
 
 
 def test_library_exports_every_declared_symbol():
@@ -114,3 +115,16 @@ def test_fwd_opts_validate_before_any_launch():
     # misaligned block table
     o = _lib.DsaFwdOptions(block_size=64, max_blocks=16, num_blocks=100, block_table=ctypes.c_void_p((1 << 20) + 2))
     assert _opts_call(lib, o, L=1024) < 0 and b"aligned" in lib.dsa_last_error()
+
+
+def test_indexer_entry_points_validate_before_any_launch():
+    lib = _lib.load()
+    fake = ctypes.c_void_p(1 << 20)
+    assert lib.dsa_indexer_logits(None, fake, fake, fake, fake, 1, 1, 64, 100, None) < 0
+    assert lib.dsa_indexer_logits(fake, fake, fake, fake, fake, 1, 1, 48, 100, None) < 0
+    assert b"32 or 64" in lib.dsa_last_error()
+    assert lib.dsa_indexer_logits(fake, fake, fake, fake, fake, 1, 1, 64, 1 << 24, None) < 0
+    assert lib.dsa_indexer_logits(fake, ctypes.c_void_p((1 << 20) + 8), fake, fake, fake, 1, 1, 64, 100, None) < 0
+    assert b"aligned" in lib.dsa_last_error()
+    assert lib.dsa_indexer_topk(fake, fake, None, 1, 1, 100, 10, None) < 0
+    assert lib.dsa_indexer_topk(fake, fake, fake, 1, 1, 100, 0, None) < 0

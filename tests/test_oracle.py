@@ -14,6 +14,7 @@ import math
 import os
 from pathlib import Path
 
+import numpy as np
 import pytest
 import torch
 
@@ -313,3 +314,86 @@ def test_unpage_matches_elementwise_gather_and_masks_holes():
                 v = int(ids[b, s, 0, j])
                 hole = 0 <= v < 96 and not bool(ok[b, v])
                 assert int(masked[b, s, 0, j]) == (-1 if hole else v)
+
+
+# ------------------------------------------------------- lightning indexer (no reference counterpart)
+def _indexer_small(seed, batch=2, queries=3, heads=32, length=50):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(batch, queries, heads, 128, generator=g).bfloat16()
+    k = torch.randn(batch, length, 128, generator=g).bfloat16()
+    w = torch.randn(batch, queries, heads, generator=g)
+    lengths = torch.randint(0, length + 5, (batch, queries), generator=g, dtype=torch.int32)
+    return q, k, w, lengths
+
+
+def _logits_brute(q, k, w, lengths):
+    batch, queries, heads, _ = q.shape
+    length = k.shape[1]
+    out = torch.full((batch, queries, length), -float("inf"), dtype=torch.float64)
+    for b in range(batch):
+        for t in range(queries):
+            for s in range(min(int(lengths[b, t]), length)):
+                acc = 0.0
+                for j in range(heads):
+                    dot = float((q[b, t, j].double() * k[b, s].double()).sum())
+                    acc += float(w[b, t, j]) * max(dot, 0.0)
+                out[b, t, s] = acc
+    return out
+
+
+def test_indexer_logits_matches_brute_force():
+    q, k, w, lengths = _indexer_small(21)
+    ref = O.indexer_logits_ref(q, k, w, lengths)
+    brute = _logits_brute(q, k, w, lengths)
+    finite = torch.isfinite(brute)
+    assert torch.equal(torch.isfinite(ref), finite)
+    torch.testing.assert_close(ref.double()[finite], brute[finite], rtol=1e-5, atol=1e-4)
+
+
+def test_indexer_planted_mistakes_are_caught():
+    q, k, w, lengths = _indexer_small(22)
+    brute = _logits_brute(q, k, w, lengths)
+    finite = torch.isfinite(brute)
+    no_relu = torch.einsum("bthd,bsd->bts", q.float() * w[..., None], k.float()).double()
+    no_weight = torch.einsum("bthd,bsd->bths", q.float(), k.float()).clamp_min(0).sum(2).double()
+    for wrong in (no_relu, no_weight):
+        assert not torch.allclose(wrong[finite], brute[finite], rtol=1e-3, atol=1e-3)
+
+
+def _topk_brute(logits, lengths, topk):
+    batch, queries, length = logits.shape
+    out = torch.full((batch, queries, 1, topk), -1, dtype=torch.int32)
+    for b in range(batch):
+        for t in range(queries):
+            n = min(max(int(lengths[b, t]), 0), length)
+            keys = O.float_key(logits[b, t, :n].numpy())
+            ranked = sorted(range(n), key=lambda s: (-int(keys[s]), s))[:topk]
+            for j, s in enumerate(sorted(ranked)):
+                out[b, t, 0, j] = s
+    return out
+
+
+def test_float_key_orders_like_floats():
+    vals = np.array([-np.inf, -3.5, -1e-30, -0.0, 0.0, 1e-30, 2.0, np.inf], dtype=np.float32)
+    keys = O.float_key(vals)
+    assert list(np.argsort(keys, kind="stable")) == list(range(len(vals)))
+    assert keys[3] < keys[4]  # -0.0 below +0.0
+
+
+@pytest.mark.parametrize("topk", [1, 7, 40, 64])
+def test_indexer_topk_matches_brute_force_with_ties(topk):
+    g = torch.Generator().manual_seed(23)
+    logits = (torch.randint(-4, 5, (2, 5, 60), generator=g).float() / 2)  # many ties
+    logits[0, 1, 10:20] = -0.0
+    logits[0, 1, 20:30] = 0.0
+    logits[1, 2, :] = -float("inf")
+    lengths = torch.tensor([[60, 35, 0, 61, 7], [1, 60, 60, 20, 59]], dtype=torch.int32)
+    assert torch.equal(O.indexer_topk_ref(logits, lengths, topk), _topk_brute(logits, lengths, topk))
+
+
+def test_indexer_topk_planted_tie_order_is_caught():
+    logits = torch.zeros(1, 1, 10)
+    lengths = torch.tensor([[10]], dtype=torch.int32)
+    got = O.indexer_topk_ref(logits, lengths, 3)
+    assert got[0, 0, 0].tolist() == [0, 1, 2]  # ties keep the lowest s
+    assert got[0, 0, 0].tolist() != [7, 8, 9]
