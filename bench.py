@@ -40,7 +40,8 @@ sys.path.insert(0, str(ROOT))
 
 import dsa_amd  # noqa: E402
 from dsa_amd import Tuning, _lib  # noqa: E402
-from dsa_amd.workloads import BASELINE_CONFIGS, baseline_inputs  # noqa: E402
+from dsa_amd.workloads import (BASELINE_CONFIGS, INDEXER_CONFIGS, baseline_inputs,  # noqa: E402
+                               indexer_inputs)
 
 METRIC = json.loads((ROOT / "BASELINE.json").read_text())["metric"]
 HBM_PEAK_GBS = 8000.0
@@ -275,6 +276,139 @@ def run(name, args):
     return line
 
 
+# ---------------------------------------------------------------- indexer
+# Input sets cycled per indexer workload: decode_b8's keys (64 MiB a set) are
+# rotated over 512 MiB, twice the MALL; the MTP case reads 1 GiB of keys a call.
+INDEXER_ROTATE = {"idx_decode_b8": 8, "idx_decode_mtp_b64": 1, "idx_prefill_4k": 1}
+INDEXER_BOUND = {"idx_decode_b8": "hbm", "idx_decode_mtp_b64": "hbm", "idx_prefill_4k": "mfma"}
+
+
+def indexer_units(name, lengths):
+    """Algorithmic bytes and FLOPs of one logits launch: every key read once
+    (B*L rows of 128 bf16), queries and weights read once, every defined
+    logit written once (4 B); 2*HI*128 MFMA FLOPs per defined (query, key)."""
+    b, sq, hi, length, _, _ = INDEXER_CONFIGS[name]
+    pairs = int(lengths.clamp(0, length).sum())
+    nbytes = b * length * 128 * 2 + b * sq * hi * (128 * 2 + 4) + pairs * 4
+    return nbytes, 2 * hi * 128 * pairs
+
+
+class IndexerCall:
+    """One preallocated indexer call (logits + top-k) through the C ABI."""
+
+    def __init__(self, data, topk):
+        self.data = data
+        q, k, w, lengths = data
+        self.shape = (q.shape[0], q.shape[1], q.shape[2], k.shape[1], topk)
+        self.logits = torch.empty((q.shape[0], q.shape[1], k.shape[1]), device=q.device, dtype=torch.float32)
+        self.indices = torch.empty((q.shape[0], q.shape[1], 1, topk), device=q.device, dtype=torch.int32)
+        p = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+        self.largs = [p(q), p(k), p(w), p(lengths), p(self.logits)]
+        self.targs = [p(self.logits), p(lengths), p(self.indices)]
+        self.lib = _lib.load()
+
+    def main(self, stream):
+        b, sq, hi, length, _ = self.shape
+        rc = self.lib.dsa_indexer_logits(*self.largs, b, sq, hi, length, stream)
+        if rc:
+            _lib.check(rc, "dsa_indexer_logits")
+
+    def merge(self, stream):  # the second launch of a call: the selection
+        b, sq, _, length, topk = self.shape
+        rc = self.lib.dsa_indexer_topk(*self.targs, b, sq, length, topk, stream)
+        if rc:
+            _lib.check(rc, "dsa_indexer_topk")
+
+
+def indexer_cpu_baseline(name, data, budget_s=10.0):
+    """The CPU oracle (logits + selection) on an evenly spaced query sample,
+    scaled by the sample's share of (query, key) pairs."""
+    from oracle import dsa_oracle as oracle
+
+    q, k, w, lengths = (t.cpu() for t in data)
+    topk = INDEXER_CONFIGS[name][4]
+    batch, queries = q.shape[:2]
+
+    def run_rows(rows):
+        for b, sl in rows:
+            lg = oracle.indexer_logits_ref(q[b:b + 1, sl], k[b:b + 1], w[b:b + 1, sl], lengths[b:b + 1, sl])
+            oracle.indexer_topk_ref(lg, lengths[b:b + 1, sl], topk)
+
+    probe_t = time.perf_counter()
+    run_rows([(0, slice(0, 1))])
+    per_query = max(time.perf_counter() - probe_t, 1e-4)
+    n = max(1, min(batch * queries, int(budget_s / 3 / per_query)))
+    flat = list(range(0, batch * queries, max(1, batch * queries // n)))[:n]
+    rows = [(i // queries, slice(i % queries, i % queries + 1)) for i in flat]
+    pairs_all = float(lengths.clamp(0, k.shape[1]).sum())
+    pairs_sample = float(sum(min(int(lengths[b, sl][0]), k.shape[1]) for b, sl in rows))
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while time.perf_counter() < t_end or len(times) < 2:
+        t0 = time.perf_counter()
+        run_rows(rows)
+        times.append(time.perf_counter() - t0)
+        if len(times) >= 20:
+            break
+    per_call_us = statistics.median(times) * 1e6 * pairs_all / pairs_sample
+    return {"value": round(per_call_us, 1), "unit": "µs/call", "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": (f"FP32 torch indexer logits + numpy top-k oracle on {len(rows)} of {batch * queries} "
+                       f"queries of one {name} call, median of {len(times)} runs, scaled by (query, key) pairs")}
+
+
+def run_indexer(name, args):
+    b, sq, hi, length, topk, causal = INDEXER_CONFIGS[name]
+    rotate = args.rotate if args.rotate else INDEXER_ROTATE[name]
+    print(f"[bench] {name} B={b} SQ={sq} HI={hi} L={length} TOPK={topk} causal={causal} rotate={rotate}",
+          file=sys.stderr, flush=True)
+    sets = [indexer_inputs(name, seed=args.seed + i, device="cuda") for i in range(rotate)]
+    calls = [IndexerCall(d, topk) for d in sets]
+    wall, logits_us, topk_us, span_us = time_calls(calls, args.steps, args.warmup)
+    _, warm_logits, _, warm_span = time_calls(calls[:1], args.steps, args.warmup)
+    nbytes, flops = indexer_units(name, sets[0][3])
+    bound = INDEXER_BOUND[name]
+    if bound == "hbm":
+        achieved, peak, unit = nbytes / (logits_us * 1e-6) / 1e9, HBM_PEAK_GBS, "GB/s"
+    else:
+        achieved, peak, unit = flops / (logits_us * 1e-6) / 1e12, MFMA_PEAK_TFLOPS, "TFLOP/s"
+    traffic = ROOT / "profiles" / f"indexer_logits_{name}_hbm_traffic.json"
+    line = {
+        "metric": "lightning indexer span (index logits + top-k selection)",
+        "value": round(span_us, 3),
+        "unit": "µs/call",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall * 1e3 / args.steps, 5),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": (f"synthetic: seeded N(0,1) bf16 index queries/keys, N(0,0.01) fp32 head weights, "
+                 f"{'causal' if causal else 'decode'} lengths, {rotate} rotating input set(s) resident in HBM"),
+        "config": {"workload": name, "B": b, "SQ": sq, "HI": hi, "L": length, "TOPK": topk,
+                   "rotating_input_sets": rotate},
+        "roofline": {"bound": bound, "achieved": round(achieved, 2), "peak": peak, "unit": unit,
+                     "frac": round(achieved / peak, 4),
+                     "traffic": (json.loads(traffic.read_text()).get("hbm_bytes_per_launch")
+                                 if traffic.exists() else None),
+                     "kernel": f"indexer_logits, {nbytes} algorithmic B and {flops} FLOP per launch"},
+        "breakdown": {
+            "span_us": round(span_us, 3),
+            "logits_us": round(logits_us, 3),
+            "topk_us": round(topk_us, 3),
+            "warm_span_us": round(warm_span, 3),
+            "warm_logits_us": round(warm_logits, 3),
+            "logits_TBps": round(nbytes / (logits_us * 1e-6) / 1e12, 3),
+            "logits_TFLOPs": round(flops / (logits_us * 1e-6) / 1e12, 2),
+        },
+    }
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = indexer_cpu_baseline(name, sets[0], args.cpu_budget)
+    return line
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -287,6 +421,8 @@ def main():
     ap.add_argument("--seed", type=int, default=20261102)
     ap.add_argument("--paged", type=int, default=0, metavar="BLOCK",
                     help="run the workload on paged kv (block pools of BLOCK rows, random block table)")
+    ap.add_argument("--indexer", default="", metavar="WORKLOAD",
+                    help="time the lightning indexer instead: " + ", ".join(INDEXER_CONFIGS) + " or all")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU oracle timing")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
@@ -308,6 +444,12 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         print(json.dumps({"calibration_copy_bytes": n * 4, "copies": 5}))
+        return
+    if args.indexer:
+        for name in list(INDEXER_CONFIGS) if args.indexer == "all" else [args.indexer]:
+            if name not in INDEXER_CONFIGS:
+                raise SystemExit(f"unknown indexer workload {name!r}")
+            print(json.dumps(run_indexer(name, args), ensure_ascii=False), flush=True)
         return
     names = ["c2_decode_b8", "c3_decode_h16_mtp", "c4_prefill_h16", "c5_prefill_h128"] if args.all else [args.config]
     for name in names:

@@ -331,7 +331,8 @@ int dsa_indexer_logits(const uint16_t* q_idx, const uint16_t* k_idx, const float
     p.tiles_per_wg = (int)((work + 1023) / 1024);
     if (p.tiles_per_wg < 1) p.tiles_per_wg = 1;
     if (p.tiles_per_wg > p.ntiles) p.tiles_per_wg = p.ntiles;
-    if ((int64_t)B * p.tgroups > 0x7fffffff) return fail(-1, "grid too large");
+    // grid.x * 256 work-items must stay below 2^32
+    if ((int64_t)B * p.tgroups >= (1 << 24)) return fail(-1, "too many query groups (B * ceil(SQ * HI / 256))");
     const int rc = dsa::launch_indexer_logits(p, stream);
     if (rc) return hip_fail(rc, "indexer logits launch");
     g_err[0] = 0;
@@ -343,7 +344,8 @@ int dsa_indexer_topk(const float* logits, const int32_t* lengths, int32_t* indic
     if (!logits || !lengths || !indices) return fail(-1, "NULL pointer argument");
     if (B <= 0 || SQ <= 0 || L <= 0 || TOPK <= 0)
         return fail(-1, "B, SQ, L, TOPK must be positive (got %d, %d, %d, %d)", B, SQ, L, TOPK);
-    if ((int64_t)B * SQ > 0x7fffffff) return fail(-1, "too many rows");
+    // one 1024-thread workgroup per row: rows * 1024 work-items below 2^32
+    if ((int64_t)B * SQ >= (1 << 22)) return fail(-1, "B * SQ must be below 4194304 (got %lld)", (long long)B * SQ);
     const int rc = dsa::launch_indexer_topk(logits, lengths, indices, B * SQ, L, TOPK, stream);
     if (rc) return hip_fail(rc, "indexer top-k launch");
     g_err[0] = 0;

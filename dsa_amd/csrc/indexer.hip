@@ -17,12 +17,15 @@
 // LDS), then the ReLU and the weighted sum over heads in registers: each lane
 // holds 16 heads of one key, its partner lane (l ^ 32) the other 16.
 //
-// Top-k kernel: one 1024-thread workgroup per query row.  A 4-pass radix
-// select (8 bits per pass, LDS histograms) over order-preserving 32-bit keys
-// of the logits finds the TOPK-th largest key T; a compaction pass then keeps
-// every s with key > T and the lowest-s ties == T, writing them in ascending
-// order with block-wide prefix counts.  Rows of up to 32768 candidates are
-// cached in LDS after the first read.
+// Top-k kernel: one 1024-thread workgroup per query row.  A radix select over
+// order-preserving 32-bit keys of the logits finds the TOPK-th largest key T:
+// a 12-bit first digit over every candidate (4096 LDS bins, wide enough that
+// the atomics of clustered logits rarely collide), a 4-bit digit over the
+// LDS-cached upper halves of the keys, then two 8-bit digits over the few
+// entries that share T's upper 16 bits, gathered into LDS.  One sweep keeps
+// every s with key > T and the lowest-s ties == T, written in ascending
+// order.  A row of up to 65536 candidates is read from memory once, plus its
+// gathered entries.
 #include <hip/hip_runtime.h>
 #include <float.h>
 #include <stdint.h>
@@ -225,7 +228,21 @@ __global__ __launch_bounds__(256, 1) void indexer_logits_kernel(IndexerParams p)
 
 // ------------------------------------------------------------------ top-k
 constexpr int kTopkThreads = 1024;
-constexpr int kCacheKeys = 32768;  // candidates kept in LDS (128 KiB)
+constexpr int kTopkWaves = kTopkThreads / 64;
+constexpr int kChunk = 256;        // entries one wave covers per step: 4 consecutive per lane
+constexpr int kCacheKeys = 65536;  // bits 31..16 of every candidate's key cached in LDS (128 KiB)
+constexpr int kBins0 = 4096;       // first digit: key bits 31..20 (sign, exponent, 3 mantissa bits)
+constexpr int kCandCap = 1536;     // entries sharing T's upper 16 bits kept in LDS as (s, key)
+
+struct TopkShared {
+    __attribute__((aligned(16))) uint16_t hi16[kCacheKeys];
+    uint32_t hist[kBins0];  // digit histograms; afterwards 2 flag bits per cached s
+    uint32_t cand_s[kCandCap];
+    uint32_t cand_key[kCandCap];
+    uint32_t wgt[kTopkWaves];  // per wave segment: entries with key > T
+    uint32_t weq[kTopkWaves];  // per wave segment: entries with key == T
+    uint32_t word[4];
+};
 
 // Order-preserving map of a float to an unsigned key (larger float, larger key).
 __device__ __forceinline__ uint32_t float_key(float f) {
@@ -233,109 +250,379 @@ __device__ __forceinline__ uint32_t float_key(float f) {
     return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
-__global__ __launch_bounds__(kTopkThreads, 1) void indexer_topk_kernel(const float* __restrict__ logits,
-                                                                      const int32_t* __restrict__ len,
-                                                                      int32_t* __restrict__ out, int L, int K) {
-    __shared__ uint32_t cache[kCacheKeys];
-    __shared__ uint32_t hist[256];
-    __shared__ uint32_t wave_cnt[2][kTopkThreads / 64];
-    __shared__ uint32_t shared_word[4];
-    const int row = blockIdx.x;
+__device__ __forceinline__ uint64_t lanes_below(int lane) { return lane == 0 ? 0ull : (~0ull >> (64 - lane)); }
+
+__device__ __forceinline__ uint32_t wave_sum(uint32_t v) {
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) v += __shfl_xor(v, d);
+    return v;
+}
+
+// Inclusive prefix sum across the wave (lane order).
+__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v, int lane) {
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const uint32_t o = __shfl_up(v, d);
+        if (lane >= d) v += o;
+    }
+    return v;
+}
+
+// Keys of entries s .. s + 3 (s a multiple of 4) below `end`; 0 past it.
+__device__ __forceinline__ void load_keys4(const float* __restrict__ src, int s, int end, bool aligned,
+                                           uint32_t k[4]) {
+    if (aligned && s + 3 < end) {
+        const float4 v = *reinterpret_cast<const float4*>(src + s);
+        k[0] = float_key(v.x);
+        k[1] = float_key(v.y);
+        k[2] = float_key(v.z);
+        k[3] = float_key(v.w);
+    } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) k[j] = s + j < end ? float_key(src[s + j]) : 0u;
+    }
+}
+
+// Per row: the threshold key T (the K-th largest key) and the number of
+// entries equal to T to take, found digit by digit, then one sweep that
+// writes the selected s in ascending order.  Each wave owns a contiguous
+// segment of s, walked 256 entries (4 per lane) at a time.
+//   digit 0, bits 31..20: one read of the row; caches the keys' bits 31..16
+//   digit 1, bits 19..16: entries of digit 0's bin, from the cache; also
+//           counts per segment the entries whose upper 16 bits exceed T's
+//   gather: the entries sharing T's upper 16 bits (typically a few hundred)
+//           as (s, key) into LDS -- one batch of independent loads
+//   digits 2, 3, bits 15..8 and 7..0: over the gathered entries, which then
+//           get flags (key > T, key == T) and per-segment counts
+//   sweep: the segment counts place every wave's writes.
+// CACHED = false (rows longer than the cache) reads the row from memory in
+// every pass; a 16-bit prefix shared by more than kCandCap entries is
+// resolved over the whole row, reading keys from memory.
+template <bool CACHED>
+__device__ __forceinline__ void topk_select(TopkShared& sh, const float* __restrict__ src, int32_t* __restrict__ dst,
+                                            int n, int K, bool aligned) {
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
-    const int n = min(max(len[row], 0), L);
-    const float* src = logits + (int64_t)row * L;
-    int32_t* dst = out + (int64_t)row * K;
+    const uint64_t below = lanes_below(lane);
+    const int seg = (n + kTopkWaves * kChunk - 1) / (kTopkWaves * kChunk) * kChunk;
+    const int lo = min(wave * seg, n), hi = min(lo + seg, n);  // this wave's entries [lo, hi)
 
-    if (n <= K) {  // every candidate is selected
-        for (int j = tid; j < K; j += kTopkThreads) dst[j] = j < n ? j : -1;
-        return;
-    }
-    const bool cached = n <= kCacheKeys;
-    auto key_at = [&](int s) -> uint32_t { return cached ? cache[s] : float_key(src[s]); };
+    // Upper key halves of entries s .. s + 3 (0 past the segment: callers mask with s + j < hi).
+    auto hi4 = [&](int s, uint32_t h[4]) {
+        if constexpr (CACHED) {
+            const uint2 v = *reinterpret_cast<const uint2*>(&sh.hi16[s]);
+            h[0] = v.x & 0xffffu;
+            h[1] = v.x >> 16;
+            h[2] = v.y & 0xffffu;
+            h[3] = v.y >> 16;
+        } else {
+            uint32_t k[4];
+            load_keys4(src, s, hi, aligned, k);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) h[j] = k[j] >> 16;
+        }
+    };
 
-    uint32_t prefix = 0, mask = 0;
-    int remaining = K;  // keys still to take among those matching prefix under mask
-#pragma unroll 1
-    for (int pass = 0; pass < 4; ++pass) {
-        const int shift = 24 - 8 * pass;
-        for (int i = tid; i < 256; i += kTopkThreads) hist[i] = 0;
-        __syncthreads();
-        for (int s = tid; s < n; s += kTopkThreads) {
-            uint32_t u;
-            if (pass == 0) {
-                u = float_key(src[s]);
-                if (cached) cache[s] = u;
-            } else {
-                u = key_at(s);
+    // ---- digit 0 (bits 31..20) over every candidate; caches bits 31..16
+    for (int i = tid; i < kBins0; i += kTopkThreads) sh.hist[i] = 0;
+    if (tid < kTopkWaves) sh.weq[tid] = 0;
+    if (tid == 0) sh.word[2] = 0;
+    __syncthreads();
+    {
+        constexpr int U = 8;  // loads in flight per lane
+        for (int base = lo; base < hi; base += U * kChunk) {
+            uint32_t k[U][4];
+#pragma unroll
+            for (int u = 0; u < U; ++u) load_keys4(src, base + u * kChunk + 4 * lane, hi, aligned, k[u]);
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int s = base + u * kChunk + 4 * lane;
+                if (s < hi) {
+                    if constexpr (CACHED)
+                        *reinterpret_cast<uint2*>(&sh.hi16[s]) =
+                            make_uint2((k[u][0] >> 16) | (k[u][1] & 0xffff0000u), (k[u][2] >> 16) | (k[u][3] & 0xffff0000u));
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        if (s + j < hi) atomicAdd(&sh.hist[k[u][j] >> 20], 1u);
+                }
             }
-            if ((u & mask) == prefix) atomicAdd(&hist[(u >> shift) & 255], 1u);
+        }
+    }
+    __syncthreads();
+    uint32_t need = (uint32_t)K;  // entries still to take among those matching the digits so far
+    {
+        // thread tid owns bins kBins0 - 1 - 4 tid - j (j = 0..3), counted from the top
+        uint32_t c[4], mine = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            c[j] = sh.hist[kBins0 - 1 - 4 * tid - j];
+            mine += c[j];
+        }
+        const uint32_t incl = wave_incl_scan(mine, lane);
+        if (lane == 63) sh.wgt[wave] = incl;
+        __syncthreads();
+        uint32_t above = incl - mine;
+        for (int w = 0; w < wave; ++w) above += sh.wgt[w];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            if (above < need && above + c[j] >= need) {  // exactly one (thread, j) crosses
+                sh.word[0] = (uint32_t)(kBins0 - 1 - 4 * tid - j);
+                sh.word[1] = above;
+            }
+            above += c[j];
         }
         __syncthreads();
-        if (wave == 0) {
-            // Suffix counts over the 256 bins, four bins per lane from the top.
+    }
+    const uint32_t bin0 = sh.word[0];
+    need -= sh.word[1];
+    __syncthreads();  // hist, word and wgt are rewritten below
+
+    // ---- digit 1 (bits 19..16): per-wave 16-bin histograms of digit 0's bin
+    if (tid < kTopkWaves * 16) sh.hist[tid] = 0;
+    __syncthreads();
+    {
+        uint32_t above0 = 0;  // entries of this segment in bins above bin0
+        constexpr int U = CACHED ? 4 : 8;
+        for (int base = lo; base < hi; base += U * kChunk) {
+            uint32_t h[U][4];
+#pragma unroll
+            for (int u = 0; u < U; ++u) hi4(base + u * kChunk + 4 * lane, h[u]);
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int s = base + u * kChunk + 4 * lane;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    if (s + j < hi) {
+                        const uint32_t d0 = h[u][j] >> 4;
+                        above0 += d0 > bin0 ? 1u : 0u;
+                        if (d0 == bin0) atomicAdd(&sh.hist[wave * 16 + (h[u][j] & 15u)], 1u);
+                    }
+                }
+            }
+        }
+        above0 = wave_sum(above0);
+        if (lane == 0) sh.wgt[wave] = above0;
+    }
+    __syncthreads();
+    if (wave == 0) {  // lane l < 16 holds bin 15 - l
+        uint32_t c = 0;
+        if (lane < 16)
+            for (int w = 0; w < kTopkWaves; ++w) c += sh.hist[w * 16 + 15 - lane];
+        const uint32_t above = wave_incl_scan(c, lane) - c;
+        if (lane < 16 && above < need && above + c >= need) {
+            sh.word[0] = 15 - lane;
+            sh.word[1] = above;
+            sh.word[3] = c;
+        }
+    }
+    __syncthreads();
+    const uint32_t digit1 = sh.word[0];
+    const uint32_t pre16 = (bin0 << 4) | digit1;
+    const uint32_t in16 = sh.word[3];
+    need -= sh.word[1];
+    if (tid < kTopkWaves) {  // segment counts of entries whose upper 16 bits exceed pre16
+        uint32_t c = sh.wgt[tid];
+        for (uint32_t d = digit1 + 1; d < 16; ++d) c += sh.hist[tid * 16 + d];
+        sh.wgt[tid] = c;
+    }
+    __syncthreads();
+
+    // ---- gather the entries sharing the 16-bit prefix (when they fit)
+    const bool gathered = in16 <= (uint32_t)kCandCap;
+    if (gathered) {
+        constexpr int U = CACHED ? 4 : 8;
+        for (int base = lo; base < hi; base += U * kChunk) {
+            uint32_t h[U][4];
+#pragma unroll
+            for (int u = 0; u < U; ++u) hi4(base + u * kChunk + 4 * lane, h[u]);
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int s = base + u * kChunk + 4 * lane;
+                bool hit[4];
+                uint32_t total = 0, off = 0;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    hit[j] = s + j < hi && h[u][j] == pre16;
+                    const uint64_t m = __ballot(hit[j]);
+                    total += (uint32_t)__popcll(m);
+                    off += (uint32_t)__popcll(m & below);
+                }
+                if (total) {  // wave-uniform
+                    uint32_t at = 0;
+                    if (lane == 0) at = atomicAdd(&sh.word[2], total);
+                    at = __shfl(at, 0) + off;
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        if (hit[j]) sh.cand_s[at++] = (uint32_t)(s + j);
+                }
+            }
+        }
+        __syncthreads();
+        for (int i = tid; i < (int)in16; i += kTopkThreads) sh.cand_key[i] = float_key(src[sh.cand_s[i]]);
+        __syncthreads();
+    }
+
+    // ---- digits 2, 3 (bits 15..8, 7..0) over the gathered entries (else over the row)
+    uint32_t prefix = pre16 << 16, mask = 0xffff0000u;
+#pragma unroll 1
+    for (int shift = 8; shift >= 0; shift -= 8) {
+        if (tid < 256) sh.hist[tid] = 0;
+        __syncthreads();
+        if (gathered) {
+            for (int i = tid; i < (int)in16; i += kTopkThreads) {
+                const uint32_t u = sh.cand_key[i];
+                if ((u & mask) == prefix) atomicAdd(&sh.hist[(u >> shift) & 255], 1u);
+            }
+        } else {
+            for (int s = tid; s < n; s += kTopkThreads) {
+                const uint32_t u = float_key(src[s]);
+                if ((u & mask) == prefix) atomicAdd(&sh.hist[(u >> shift) & 255], 1u);
+            }
+        }
+        __syncthreads();
+        if (wave == 0) {  // four bins per lane from the top
             uint32_t c[4], sum = 0;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                c[j] = hist[255 - (4 * lane + j)];
+                c[j] = sh.hist[255 - (4 * lane + j)];
                 sum += c[j];
             }
-            // inclusive scan of the per-lane sums across the wave (bins from the top)
-            uint32_t incl = sum;
-#pragma unroll
-            for (int d = 1; d < 64; d <<= 1) {
-                const uint32_t o = __shfl_up(incl, d);
-                if (lane >= d) incl += o;
-            }
-            uint32_t above = incl - sum;  // keys in bins above this lane's four
+            uint32_t above = wave_incl_scan(sum, lane) - sum;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                if (above < (uint32_t)remaining && above + c[j] >= (uint32_t)remaining) {
-                    shared_word[0] = 255 - (4 * lane + j);  // the bin holding the remaining-th key
-                    shared_word[1] = above;
+                if (above < need && above + c[j] >= need) {
+                    sh.word[0] = 255 - (4 * lane + j);
+                    sh.word[1] = above;
                 }
                 above += c[j];
             }
         }
         __syncthreads();
-        const uint32_t digit = shared_word[0];
-        remaining -= (int)shared_word[1];
-        prefix |= digit << shift;
+        need -= sh.word[1];
+        prefix |= sh.word[0] << shift;
         mask |= 255u << shift;
-        __syncthreads();  // shared_word is rewritten by the next pass
+        __syncthreads();  // word and hist are rewritten next
     }
-    // Threshold key T = prefix; `remaining` ties (key == T) are taken, lowest s first.
     const uint32_t thr = prefix;
-    uint32_t taken = 0, ties = 0;  // running totals over the chunks before this one
-#pragma unroll 1
-    for (int base = 0; base < n; base += kTopkThreads) {
-        const int s = base + tid;
-        const uint32_t u = s < n ? key_at(s) : 0u;
-        const bool tie = s < n && u == thr;
-        const uint64_t tie_mask = __ballot(tie);
-        const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-        const uint32_t tie_rank_wave = (uint32_t)__popcll(tie_mask & below);
-        if (lane == 0) wave_cnt[0][wave] = (uint32_t)__popcll(tie_mask);
-        __syncthreads();
-        uint32_t tie_before = ties;
-        for (int w = 0; w < wave; ++w) tie_before += wave_cnt[0][w];
-        const bool sel = s < n && (u > thr || (tie && tie_before + tie_rank_wave < (uint32_t)remaining));
-        const uint64_t sel_mask = __ballot(sel);
-        if (lane == 0) wave_cnt[1][wave] = (uint32_t)__popcll(sel_mask);
-        __syncthreads();
-        uint32_t pos = taken + (uint32_t)__popcll(sel_mask & below);
-        uint32_t chunk_sel = 0, chunk_tie = 0;
-        for (int w = 0; w < kTopkThreads / 64; ++w) {
-            if (w < wave) pos += wave_cnt[1][w];
-            chunk_sel += wave_cnt[1][w];
-            chunk_tie += wave_cnt[0][w];
+
+    // ---- segment counts (and, for a cached row, flags) of the entries sharing pre16
+    const bool flags = CACHED && gathered;
+    if (flags)
+        for (int i = tid; i < kBins0; i += kTopkThreads) sh.hist[i] = 0;
+    __syncthreads();
+    if (gathered) {
+        for (int i = tid; i < (int)in16; i += kTopkThreads) {
+            const uint32_t u = sh.cand_key[i], s = sh.cand_s[i];
+            const int w = (int)s / seg;
+            if (u > thr) atomicAdd(&sh.wgt[w], 1u);
+            if (u == thr) atomicAdd(&sh.weq[w], 1u);
+            if (flags) {
+                const uint32_t f = (u > thr ? 1u : 0u) | (u == thr ? 2u : 0u);
+                if (f) atomicOr(&sh.hist[s >> 4], f << (2 * (s & 15)));
+            }
         }
-        if (sel && pos < (uint32_t)K) dst[pos] = s;
-        taken += chunk_sel;
-        ties += chunk_tie;
-        __syncthreads();  // wave_cnt is rewritten by the next chunk
+    } else {
+        uint32_t ng = 0, ne = 0;
+        for (int s = lo + lane; s < hi; s += 64) {
+            const uint32_t u = float_key(src[s]);
+            ng += (u >> 16) == pre16 && u > thr ? 1u : 0u;
+            ne += u == thr ? 1u : 0u;
+        }
+        ng = wave_sum(ng);
+        ne = wave_sum(ne);
+        if (lane == 0) {
+            sh.wgt[wave] += ng;
+            sh.weq[wave] = ne;
+        }
     }
+    __syncthreads();
+
+    // ---- output: every s with key > T, then the first `need` with key == T, ascending s
+    uint32_t pos = 0, ties = 0;
+    for (int w = 0; w < wave; ++w) {
+        pos += sh.wgt[w];
+        ties += sh.weq[w];
+    }
+    pos += min(ties, need);
+    constexpr int U = CACHED ? 4 : 8;
+    for (int base = lo; base < hi; base += U * kChunk) {
+        uint32_t h[U][4];
+#pragma unroll
+        for (int u = 0; u < U; ++u) hi4(base + u * kChunk + 4 * lane, h[u]);
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int s = base + u * kChunk + 4 * lane;
+            bool gt[4], eq[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const bool valid = s + j < hi;
+                gt[j] = valid && h[u][j] > pre16;
+                eq[j] = false;
+                if (valid && h[u][j] == pre16) {
+                    if (flags) {
+                        const uint32_t f = sh.hist[(s + j) >> 4] >> (2 * ((s + j) & 15));
+                        gt[j] = f & 1u;
+                        eq[j] = (f >> 1) & 1u;
+                    } else {
+                        const uint32_t key = float_key(src[s + j]);
+                        gt[j] = key > thr;
+                        eq[j] = key == thr;
+                    }
+                }
+            }
+            uint32_t tie_off = 0, tie_total = 0;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const uint64_t m = __ballot(eq[j]);
+                tie_off += (uint32_t)__popcll(m & below);
+                tie_total += (uint32_t)__popcll(m);
+            }
+            bool sel[4];
+            uint32_t rank = ties + tie_off;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                sel[j] = gt[j] || (eq[j] && rank < need);
+                rank += eq[j] ? 1u : 0u;
+            }
+            uint32_t sel_off = 0, sel_total = 0;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const uint64_t m = __ballot(sel[j]);
+                sel_off += (uint32_t)__popcll(m & below);
+                sel_total += (uint32_t)__popcll(m);
+            }
+            uint32_t at = pos + sel_off;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                if (sel[j]) {
+                    if (at < (uint32_t)K) dst[at] = s + j;
+                    ++at;
+                }
+            }
+            pos += sel_total;
+            ties += tie_total;
+        }
+    }
+}
+
+__global__ __launch_bounds__(kTopkThreads, 1) void indexer_topk_kernel(const float* __restrict__ logits,
+                                                                      const int32_t* __restrict__ len,
+                                                                      int32_t* __restrict__ out, int L, int K) {
+    __shared__ TopkShared sh;
+    const int row = blockIdx.x;
+    const int n = min(max(len[row], 0), L);
+    const float* src = logits + (int64_t)row * L;
+    int32_t* dst = out + (int64_t)row * K;
+    if (n <= K) {  // every candidate is selected
+        for (int j = threadIdx.x; j < K; j += kTopkThreads) dst[j] = j < n ? j : -1;
+        return;
+    }
+    const bool aligned = (reinterpret_cast<uintptr_t>(src) & 15) == 0;
+    if (n <= kCacheKeys)
+        topk_select<true>(sh, src, dst, n, K, aligned);
+    else
+        topk_select<false>(sh, src, dst, n, K, aligned);
 }
 
 }  // namespace

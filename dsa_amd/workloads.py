@@ -121,3 +121,33 @@ def baseline_inputs(name: str, seed: int = REVIEW_SEED, device="cuda", cpu_recip
     else:
         raise ValueError(name)
     return q, kv, qr, kr, ids.reshape(batch, queries, 1, k).contiguous()
+
+
+# Lightning-indexer workloads: (B, SQ, HI, L, TOPK, causal).  The decode
+# pair feeds C2 / C3's attention (same B, SQ, L, TOPK); the prefill one is C5's
+# query block, with query i at position L - SQ + i (keys [0, L - SQ + i]).
+INDEXER_CONFIGS = {
+    "idx_decode_b8": (8, 1, 64, 32768, 2048, False),
+    "idx_decode_mtp_b64": (64, 2, 64, 65536, 2048, False),
+    "idx_prefill_4k": (1, 4096, 64, 32768, 2048, True),
+}
+
+
+def indexer_lengths(name: str, device="cuda"):
+    """Candidate keys per query ``[B, SQ]`` int32 of indexer workload ``name``:
+    query i of SQ sits at position L - SQ + i and sees keys [0, L - SQ + i]
+    (decode: the last SQ positions; prefill: causal prefixes)."""
+    batch, queries, _, length, _, _ = INDEXER_CONFIGS[name]
+    row = torch.arange(queries, device=device, dtype=torch.int32) + (length - queries + 1)
+    return row.expand(batch, queries).contiguous()
+
+
+def indexer_inputs(name: str, seed: int = REVIEW_SEED, device="cuda"):
+    """(q_idx, k_idx, weights, lengths) of indexer workload ``name``: N(0,1)
+    bf16 queries and keys, N(0, 0.1^2) fp32 head weights."""
+    batch, queries, heads, length, _, _ = INDEXER_CONFIGS[name]
+    gen = torch.Generator(device=device).manual_seed(seed)
+    q = _normal_bf16((batch, queries, heads, 128), gen, device)
+    k = _normal_bf16((batch, length, 128), gen, device)
+    w = torch.randn((batch, queries, heads), generator=gen, device=device) * 0.1
+    return q, k, w, indexer_lengths(name, device)

@@ -128,3 +128,8 @@ def test_indexer_entry_points_validate_before_any_launch():
     assert b"aligned" in lib.dsa_last_error()
     assert lib.dsa_indexer_topk(fake, fake, None, 1, 1, 100, 10, None) < 0
     assert lib.dsa_indexer_topk(fake, fake, fake, 1, 1, 100, 0, None) < 0
+    # grid limits: 256-thread workgroups per 256 query heads, 1024-thread workgroups per row
+    assert lib.dsa_indexer_logits(fake, fake, fake, fake, fake, 1 << 16, 1024, 64, 100, None) < 0
+    assert b"query groups" in lib.dsa_last_error()
+    assert lib.dsa_indexer_topk(fake, fake, fake, 1 << 11, 1 << 11, 100, 10, None) < 0
+    assert b"4194304" in lib.dsa_last_error()

@@ -4,8 +4,9 @@ ABI) with the CPU oracle.
 * logits: against the FP32 oracle, max |diff| <= 1e-4 x max |logit| over the
   defined entries (s < length); bf16 inputs, FP32 accumulation on both sides;
 * top-k: bit-exact against the oracle given the same logits (integer output),
-  including ties, -0.0 / +0.0, -inf, rows shorter than TOPK, empty rows and
-  rows longer than the 32768 keys the kernel caches in LDS;
+  including ties, -0.0 / +0.0, -inf, rows shorter than TOPK, empty rows,
+  constant rows, rows whose keys share one first-digit bin (no candidate
+  compaction) and rows longer than the 65536 keys the kernel caches in LDS;
 * end to end: the selected indices drive dsa_amd.forward, checked against the
   attention oracle on the same indices.
 """
@@ -73,8 +74,11 @@ def test_indexer_logits_parity(tag, seed, B, SQ, HI, L, mode):
 TOPK_CASES = [
     ("ties", 10, 3, 4, 3000, 512, "ties"),
     ("short rows", 11, 2, 3, 600, 2048, None),
-    ("uncached rows", 12, 1, 2, 40000, 2048, None),
+    ("long cached rows", 12, 1, 2, 40000, 2048, None),
+    ("uncached rows", 14, 1, 2, 70000, 2048, None),
     ("signed zeros and -inf", 13, 1, 2, 5000, 1000, "zeros"),
+    ("narrow values", 15, 2, 2, 20000, 2048, "narrow"),
+    ("constant rows", 16, 1, 3, 3000, 700, "constant"),
 ]
 
 
@@ -91,6 +95,10 @@ def test_indexer_topk_bit_exact(tag, seed, B, SQ, L, K, mode):
         logits[..., 1::3] = 0.0
         logits[..., 2::7] = -float("inf")
         lengths[:] = L
+    elif mode == "narrow":  # one first-digit bin holds every key: no candidate compaction
+        logits = 1.0 + logits * 1e-6
+    elif mode == "constant":
+        logits = torch.full((B, SQ, L), 0.25)
     print(f"[{tag}] launching B={B} SQ={SQ} L={L} K={K}", flush=True)
     got = dsa_amd.indexer_topk(logits.cuda(), lengths.cuda(), K)
     torch.cuda.synchronize()

@@ -181,3 +181,40 @@ def test_paged_shape_contract():
             _check_inputs(*args)
         with pytest.raises(ValueError):
             dsa_amd.forward(*args[:5], block_table=args[5])
+
+
+# ------------------------------------------------------------ lightning indexer
+def _idx_inputs(B=2, SQ=3, HI=64, L=100):
+    return (torch.zeros(B, SQ, HI, 128, dtype=torch.bfloat16), torch.zeros(B, L, 128, dtype=torch.bfloat16),
+            torch.zeros(B, SQ, HI), torch.full((B, SQ), L, dtype=torch.int32))
+
+
+@pytest.mark.parametrize("name,mutate", [
+    ("q rank", lambda a: (a[0][0],) + a[1:]),
+    ("head dim", lambda a: (a[0][..., :64],) + a[1:]),
+    ("heads 48", lambda a: (a[0][:, :, :48].contiguous(), a[1], a[2][:, :, :48].contiguous(), a[3])),
+    ("k batch", lambda a: (a[0], a[1][:1], a[2], a[3])),
+    ("weights shape", lambda a: (a[0], a[1], a[2][:, :, :32], a[3])),
+    ("lengths shape", lambda a: a[:3] + (a[3][:, :1],)),
+    ("lengths dtype", lambda a: a[:3] + (a[3].long(),)),
+    ("q dtype", lambda a: (a[0].float(),) + a[1:]),
+    ("cpu tensors", lambda a: a),
+])
+def test_indexer_logits_rejections(name, mutate):
+    with pytest.raises(ValueError):
+        dsa_amd.indexer_logits(*mutate(_idx_inputs()))
+
+
+def test_indexer_topk_rejections():
+    logits, lengths = torch.zeros(2, 3, 100), torch.full((2, 3), 100, dtype=torch.int32)
+    for bad in (0, -1, 2.0, True):
+        with pytest.raises(ValueError):
+            dsa_amd.indexer_topk(logits, lengths, bad)
+    with pytest.raises(ValueError):
+        dsa_amd.indexer_topk(logits[0], lengths, 10)
+    with pytest.raises(ValueError):
+        dsa_amd.indexer_topk(logits, lengths[:, :2], 10)
+    with pytest.raises(ValueError):
+        dsa_amd.indexer_topk(logits.double(), lengths, 10)
+    with pytest.raises(ValueError):  # CPU tensors: the selection runs on a ROCm GPU only
+        dsa_amd.indexer_topk(logits, lengths, 10)
