@@ -323,12 +323,17 @@ int dsa_indexer_logits(const uint16_t* q_idx, const uint16_t* k_idx, const float
     p.SQ = SQ;
     p.HI = HI;
     p.L = L;
-    p.tgroups = ceil_div(SQ, 256 / HI);
-    p.ntiles = ceil_div(L, 64);
-    // About 1024 workgroups: decode spreads one query's keys over many CUs,
-    // prefill keeps every key tile of a query group in one workgroup.
+    // Waves per query: all four share one query's 64 heads when SQ * HI <= 64
+    // (decode), two when <= 128, else each wave owns its own query slot.
+    p.ks = (int64_t)SQ * HI <= 64 ? 4 : ((int64_t)SQ * HI <= 128 ? 2 : 1);
+    p.tgroups = ceil_div(SQ, 256 / HI / p.ks);
+    p.ntiles = ceil_div(L, 64 * p.ks);
+    // About 1024 / ks workgroups (a stage of ks x 16 KiB, two stages per
+    // workgroup): decode spreads one query's keys over many CUs, prefill keeps
+    // every key stage of a query group in one workgroup.
     const int64_t work = (int64_t)B * p.tgroups * p.ntiles;
-    p.tiles_per_wg = (int)((work + 1023) / 1024);
+    const int64_t target = 1024 / p.ks;
+    p.tiles_per_wg = (int)((work + target - 1) / target);
     if (p.tiles_per_wg < 1) p.tiles_per_wg = 1;
     if (p.tiles_per_wg > p.ntiles) p.tiles_per_wg = p.ntiles;
     // grid.x * 256 work-items must stay below 2^32
@@ -344,6 +349,8 @@ int dsa_indexer_topk(const float* logits, const int32_t* lengths, int32_t* indic
     if (!logits || !lengths || !indices) return fail(-1, "NULL pointer argument");
     if (B <= 0 || SQ <= 0 || L <= 0 || TOPK <= 0)
         return fail(-1, "B, SQ, L, TOPK must be positive (got %d, %d, %d, %d)", B, SQ, L, TOPK);
+    // a row's bytes are addressed by a 32-bit buffer range
+    if (L >= (1 << 28)) return fail(-1, "L must be below 268435456 (got %d)", L);
     // one 1024-thread workgroup per row: rows * 1024 work-items below 2^32
     if ((int64_t)B * SQ >= (1 << 22)) return fail(-1, "B * SQ must be below 4194304 (got %lld)", (long long)B * SQ);
     const int rc = dsa::launch_indexer_topk(logits, lengths, indices, B * SQ, L, TOPK, stream);

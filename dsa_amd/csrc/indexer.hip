@@ -9,13 +9,15 @@
 // q [B, SQ, HI, 128] bf16 (HI = 32 or 64), k [B, L, 128] bf16 (one key per
 // token, shared by the heads), w [B, SQ, HI] fp32, len [B, SQ] int32.
 //
-// Logits kernel: one workgroup owns 256 / HI queries of one batch (256 query
-// heads) and a range of 64-key tiles.  Keys stream through a two-stage LDS
-// ring (buffer_load ... lds, 16 KiB per tile, 16-byte chunks XOR-swizzled by
-// row); every wave holds the Q fragments of 64 query heads in VGPRs and
-// computes C[head, key] with v_mfma_f32_32x32x16_bf16 (A = Q, B = K^T from
-// LDS), then the ReLU and the weighted sum over heads in registers: each lane
-// holds 16 heads of one key, its partner lane (l ^ 32) the other 16.
+// Logits kernel: one workgroup owns 256 / HI / KS queries of one batch and a
+// range of key stages of KS x 64 keys.  Keys stream through a two-stage LDS
+// ring (buffer_load ... lds, 16 KiB per 64 keys, 16-byte chunks XOR-swizzled
+// by row); every wave holds the Q fragments of 64 query heads in VGPRs and
+// computes C[head, key] for one 64-key sub-tile of the stage with
+// v_mfma_f32_32x32x16_bf16 (A = Q, B = K^T from LDS), then the ReLU and the
+// weighted sum over heads in registers: each lane holds 16 heads of one key,
+// its partner lane (l ^ 32) the other 16.  KS (1, 2, 4) is the number of
+// waves sharing a query: 4 for single-query decode, 1 for prefill.
 //
 // Top-k kernel: one 1024-thread workgroup per query row.  A radix select over
 // order-preserving 32-bit keys of the logits finds the TOPK-th largest key T:
@@ -97,28 +99,36 @@ __device__ __forceinline__ void load_slice(uint32_t lds_dst, rsrc_t rsrc, uint32
 #pragma clang diagnostic pop
 }
 
-template <int HI>
+// KS wave groups split every key stage (KS x 64 keys) and the workgroup's
+// 4 / KS query slots (64 query heads each) share it: KS = 1 for prefill (4
+// slots reuse each key tile), 2 or 4 when SQ is too small to fill the slots.
+template <int HI, int KS>
 __global__ __launch_bounds__(256, 1) void indexer_logits_kernel(IndexerParams p) {
     static_assert(HI == 32 || HI == 64, "indexer heads");
-    constexpr int TG = 256 / HI;  // queries per workgroup
-    __shared__ __attribute__((aligned(1024))) char smem[2 * kTileBytes];
+    static_assert(KS == 1 || KS == 2 || KS == 4, "key split");
+    constexpr int TG = 256 / HI / KS;            // queries per workgroup
+    constexpr int kStageBytes = KS * kTileBytes;  // one ring stage: KS x 64 keys
+    __shared__ __attribute__((aligned(1024))) char smem[2 * kStageBytes];
     const uint32_t lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)smem;
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int qg = wave / KS;  // this wave's query slot
+    const int kg = wave % KS;  // this wave's 64-key sub-tile of every stage
     const int b = blockIdx.x / p.tgroups;
     const int t0 = (blockIdx.x % p.tgroups) * TG;
 
-    // Key tiles of this workgroup, cut at the longest candidate range of its queries.
+    // Key stages of this workgroup, cut at the longest candidate range of its queries.
     int maxlen = 0;
 #pragma unroll
     for (int i = 0; i < TG; ++i)
         if (t0 + i < p.SQ) maxlen = max(maxlen, min(max(p.len[(int64_t)b * p.SQ + t0 + i], 0), p.L));
     const int tile_begin = blockIdx.y * p.tiles_per_wg;
-    const int tile_end = min(min(tile_begin + p.tiles_per_wg, p.ntiles), (maxlen + kKeyTile - 1) / kKeyTile);
+    const int tile_end =
+        min(min(tile_begin + p.tiles_per_wg, p.ntiles), (maxlen + kKeyTile * KS - 1) / (kKeyTile * KS));
     if (tile_begin >= tile_end) return;  // uniform: the whole workgroup leaves
 
-    // This wave's two 32-head blocks: rows (2 * wave + hb) * 32 .. + 31 of the
+    // This wave's two 32-head blocks: rows (2 * qg + hb) * 32 .. + 31 of the
     // workgroup's TG * HI query heads.  A fragments (lane: head rowbase + l % 32,
     // dims 16 ks + 8 (l / 32) .. + 7) and the weights of the 16 heads whose
     // products this lane accumulates (C row 8 (r / 4) + 4 (l / 32) + r % 4).
@@ -127,7 +137,7 @@ __global__ __launch_bounds__(256, 1) void indexer_logits_kernel(IndexerParams p)
     int tok[2], qlen[2];
 #pragma unroll
     for (int hb = 0; hb < 2; ++hb) {
-        const int rowbase = (2 * wave + hb) * 32;
+        const int rowbase = (2 * qg + hb) * 32;
         const int t = t0 + rowbase / HI;
         tok[hb] = t;
         const bool live = t < p.SQ;
@@ -143,41 +153,42 @@ __global__ __launch_bounds__(256, 1) void indexer_logits_kernel(IndexerParams p)
 
     const rsrc_t kr = make_rsrc(p.k + (int64_t)b * p.L * kDim, (uint32_t)p.L * kDim * 2u);
     auto issue = [&](int tile) {
-        const uint32_t dst = lds + (uint32_t)(tile & 1) * kTileBytes;
+        const uint32_t dst = lds + (uint32_t)(tile & 1) * kStageBytes;
 #pragma unroll
-        for (int i = 0; i < kLoadsPerWave; ++i) {
-            const int slice = wave * kLoadsPerWave + i;
-            load_slice(dst + slice * 1024, kr, (uint32_t)tile * kTileBytes, slice, lane);
+        for (int i = 0; i < kLoadsPerWave * KS; ++i) {
+            const int slice = wave * kLoadsPerWave * KS + i;
+            load_slice(dst + slice * 1024, kr, (uint32_t)tile * kStageBytes, slice, lane);
+        }
+    };
+    auto store = [&](int tile, const float (&res)[2][2]) {
+#pragma unroll
+        for (int hb = 0; hb < 2; ++hb) {
+            if constexpr (HI == 64)
+                if (hb == 1) break;  // both blocks belong to one query: summed into res[0]
+            const int t = tok[hb];
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) {
+                const int s = (tile * KS + kg) * kKeyTile + kb * 32 + (lane & 31);
+                if (lane < 32 && t < p.SQ && s < p.L)
+                    p.logits[((int64_t)b * p.SQ + t) * p.L + s] = s < qlen[hb] ? res[hb][kb] : -INFINITY;
+            }
         }
     };
 
     issue(tile_begin);
-    wait_vmcnt<0>();  // Q, weights and the first tile: nothing the compiler waits for stays in the loop
+    wait_vmcnt<0>();  // Q, weights and the first stage: nothing the compiler waits for stays in the loop
 
-    float res[2][2];  // [hb][key block] sums of the previous tile, stored one iteration late
+    float res[2][2];  // [hb][key block] sums of the previous stage, stored one iteration late
     int prev = -1;
     for (int tile = tile_begin; tile < tile_end; ++tile) {
-        wait_vmcnt<0>();  // this tile (and last iteration's stores, issued before it)
-        lds_barrier();    // tile visible; every wave is past the previous tile's reads
-        // Stores of the previous tile, then the next tile's loads (so the wait
+        wait_vmcnt<0>();  // this stage (and last iteration's stores, issued before it)
+        lds_barrier();    // stage visible; every wave is past the previous stage's reads
+        // Stores of the previous stage, then the next stage's loads (so the wait
         // above never drains a load issued after a store).
-        if (prev >= 0) {
-#pragma unroll
-            for (int hb = 0; hb < 2; ++hb) {
-                if constexpr (HI == 64)
-                    if (hb == 1) break;  // both blocks belong to one query: summed into res[0]
-                const int t = tok[hb];
-#pragma unroll
-                for (int kb = 0; kb < 2; ++kb) {
-                    const int s = prev * kKeyTile + kb * 32 + (lane & 31);
-                    if (lane < 32 && t < p.SQ && s < p.L)
-                        p.logits[((int64_t)b * p.SQ + t) * p.L + s] = s < qlen[hb] ? res[hb][kb] : -INFINITY;
-                }
-            }
-        }
+        if (prev >= 0) store(prev, res);
         if (tile + 1 < tile_end) issue(tile + 1);
 
-        const uint32_t stage = lds + (uint32_t)(tile & 1) * kTileBytes;
+        const uint32_t stage = lds + (uint32_t)(tile & 1) * kStageBytes + (uint32_t)kg * kTileBytes;
         f32x16 acc[2][2];
 #pragma unroll
         for (int hb = 0; hb < 2; ++hb)
@@ -211,19 +222,7 @@ __global__ __launch_bounds__(256, 1) void indexer_logits_kernel(IndexerParams p)
         }
         prev = tile;
     }
-    // Last tile's stores.
-#pragma unroll
-    for (int hb = 0; hb < 2; ++hb) {
-        if constexpr (HI == 64)
-            if (hb == 1) break;
-        const int t = tok[hb];
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
-            const int s = prev * kKeyTile + kb * 32 + (lane & 31);
-            if (lane < 32 && t < p.SQ && s < p.L)
-                p.logits[((int64_t)b * p.SQ + t) * p.L + s] = s < qlen[hb] ? res[hb][kb] : -INFINITY;
-        }
-    }
+    store(prev, res);  // last stage
 }
 
 // ------------------------------------------------------------------ top-k
@@ -268,25 +267,69 @@ __device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v, int lane) {
     return v;
 }
 
-// Keys of entries s .. s + 3 (s a multiple of 4) below `end`; 0 past it.
-__device__ __forceinline__ void load_keys4(const float* __restrict__ src, int s, int end, bool aligned,
-                                           uint32_t k[4]) {
-    if (aligned && s + 3 < end) {
-        const float4 v = *reinterpret_cast<const float4*>(src + s);
-        k[0] = float_key(v.x);
-        k[1] = float_key(v.y);
-        k[2] = float_key(v.z);
-        k[3] = float_key(v.w);
+// One row of logits behind a range-checked buffer descriptor: reads at or past
+// n return 0.0 (so the caller masks them), and being intrinsics the loads are
+// never wrapped in per-lane branches.
+struct Row {
+    __amdgpu_buffer_rsrc_t rs;
+    __device__ __forceinline__ uint32_t key(int s) const {
+        return float_key(__uint_as_float((uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rs, s * 4, 0, 0)));
+    }
+};
+
+// Rank of this lane among the lanes whose bit is set in m (lanes below it).
+__device__ __forceinline__ uint32_t lane_rank(uint64_t m) {
+    return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+}
+
+// Exclusive prefix over the lanes, and wave total, of a per-lane count c in
+// [0, 7]: one ballot per bit of c.
+__device__ __forceinline__ void lane_prefix3(uint32_t c, uint32_t& before, uint32_t& total) {
+    before = 0;
+    total = 0;
+#pragma unroll
+    for (int b = 0; b < 3; ++b) {
+        const uint64_t m = __ballot((c >> b) & 1u);
+        before += lane_rank(m) << b;
+        total += (uint32_t)__popcll(m) << b;
+    }
+}
+
+// 4-bit masks over entries j = 0..3: h[j] > x, h[j] == x.
+__device__ __forceinline__ uint32_t mask_gt4(const uint32_t h[4], uint32_t x) {
+    return (h[0] > x ? 1u : 0u) | (h[1] > x ? 2u : 0u) | (h[2] > x ? 4u : 0u) | (h[3] > x ? 8u : 0u);
+}
+__device__ __forceinline__ uint32_t mask_eq4(const uint32_t h[4], uint32_t x) {
+    return (h[0] == x ? 1u : 0u) | (h[1] == x ? 2u : 0u) | (h[2] == x ? 4u : 0u) | (h[3] == x ? 8u : 0u);
+}
+
+// Entries s .. s + 3 below hi, as a 4-bit mask.
+__device__ __forceinline__ uint32_t valid4(int s, int hi) {
+    const int left = hi - s;
+    return left >= 4 ? 15u : (left <= 0 ? 0u : (1u << left) - 1u);
+}
+
+// Upper key halves of entries s .. s + 3 of one wave step (s = base + 4 lane,
+// base a multiple of kChunk below hi): from the LDS cache, or from memory.
+template <bool CACHED>
+__device__ __forceinline__ void upper4(const TopkShared& sh, const Row& row, int base, int s, uint32_t h[4]) {
+    if constexpr (CACHED) {
+        (void)base;
+        const uint2 v = *reinterpret_cast<const uint2*>(&sh.hi16[s]);
+        h[0] = v.x & 0xffffu;
+        h[1] = v.x >> 16;
+        h[2] = v.y & 0xffffu;
+        h[3] = v.y >> 16;
     } else {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) k[j] = s + j < end ? float_key(src[s + j]) : 0u;
+        for (int j = 0; j < 4; ++j) h[j] = row.key(s + j) >> 16;
     }
 }
 
 // Per row: the threshold key T (the K-th largest key) and the number of
 // entries equal to T to take, found digit by digit, then one sweep that
 // writes the selected s in ascending order.  Each wave owns a contiguous
-// segment of s, walked 256 entries (4 per lane) at a time.
+// segment of s, walked kChunk entries at a time.
 //   digit 0, bits 31..20: one read of the row; caches the keys' bits 31..16
 //   digit 1, bits 19..16: entries of digit 0's bin, from the cache; also
 //           counts per segment the entries whose upper 16 bits exceed T's
@@ -299,54 +342,31 @@ __device__ __forceinline__ void load_keys4(const float* __restrict__ src, int s,
 // every pass; a 16-bit prefix shared by more than kCandCap entries is
 // resolved over the whole row, reading keys from memory.
 template <bool CACHED>
-__device__ __forceinline__ void topk_select(TopkShared& sh, const float* __restrict__ src, int32_t* __restrict__ dst,
-                                            int n, int K, bool aligned) {
+__device__ __forceinline__ void topk_select(TopkShared& sh, const Row& row, int32_t* __restrict__ dst, int n,
+                                            int K) {
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
-    const uint64_t below = lanes_below(lane);
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: segment bounds live in SGPRs
     const int seg = (n + kTopkWaves * kChunk - 1) / (kTopkWaves * kChunk) * kChunk;
     const int lo = min(wave * seg, n), hi = min(lo + seg, n);  // this wave's entries [lo, hi)
-
-    // Upper key halves of entries s .. s + 3 (0 past the segment: callers mask with s + j < hi).
-    auto hi4 = [&](int s, uint32_t h[4]) {
-        if constexpr (CACHED) {
-            const uint2 v = *reinterpret_cast<const uint2*>(&sh.hi16[s]);
-            h[0] = v.x & 0xffffu;
-            h[1] = v.x >> 16;
-            h[2] = v.y & 0xffffu;
-            h[3] = v.y >> 16;
-        } else {
-            uint32_t k[4];
-            load_keys4(src, s, hi, aligned, k);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) h[j] = k[j] >> 16;
-        }
-    };
+    constexpr int U = 4;  // wave steps per loop iteration (loads in flight)
 
     // ---- digit 0 (bits 31..20) over every candidate; caches bits 31..16
     for (int i = tid; i < kBins0; i += kTopkThreads) sh.hist[i] = 0;
     if (tid < kTopkWaves) sh.weq[tid] = 0;
     if (tid == 0) sh.word[2] = 0;
     __syncthreads();
-    {
-        constexpr int U = 8;  // loads in flight per lane
-        for (int base = lo; base < hi; base += U * kChunk) {
-            uint32_t k[U][4];
+    for (int base = lo; base < hi; base += 2 * U * kChunk) {
+        // lane-interleaved: entry base + c * 64 + lane, every load 256 contiguous bytes
+        uint32_t k[2 * U * 4];
 #pragma unroll
-            for (int u = 0; u < U; ++u) load_keys4(src, base + u * kChunk + 4 * lane, hi, aligned, k[u]);
+        for (int c = 0; c < 2 * U * 4; ++c) k[c] = row.key(base + c * 64 + lane);
 #pragma unroll
-            for (int u = 0; u < U; ++u) {
-                const int s = base + u * kChunk + 4 * lane;
-                if (s < hi) {
-                    if constexpr (CACHED)
-                        *reinterpret_cast<uint2*>(&sh.hi16[s]) =
-                            make_uint2((k[u][0] >> 16) | (k[u][1] & 0xffff0000u), (k[u][2] >> 16) | (k[u][3] & 0xffff0000u));
-#pragma unroll
-                    for (int j = 0; j < 4; ++j)
-                        if (s + j < hi) atomicAdd(&sh.hist[k[u][j] >> 20], 1u);
-                }
-            }
+        for (int c = 0; c < 2 * U * 4; ++c) {
+            const int s = base + c * 64 + lane;
+            if constexpr (CACHED)
+                if (base + (c / 4) * kChunk < hi) sh.hi16[s] = (uint16_t)(k[c] >> 16);  // step inside the cache
+            if (s < hi) atomicAdd(&sh.hist[k[c] >> 20], 1u);
         }
     }
     __syncthreads();
@@ -383,22 +403,30 @@ __device__ __forceinline__ void topk_select(TopkShared& sh, const float* __restr
     __syncthreads();
     {
         uint32_t above0 = 0;  // entries of this segment in bins above bin0
-        constexpr int U = CACHED ? 4 : 8;
         for (int base = lo; base < hi; base += U * kChunk) {
             uint32_t h[U][4];
 #pragma unroll
-            for (int u = 0; u < U; ++u) hi4(base + u * kChunk + 4 * lane, h[u]);
+            for (int u = 0; u < U; ++u) {
+                if (base + u * kChunk < hi) {
+                    upper4<CACHED>(sh, row, base + u * kChunk, base + u * kChunk + 4 * lane, h[u]);
+                } else {
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) h[u][j] = 0;
+                }
+            }
 #pragma unroll
             for (int u = 0; u < U; ++u) {
                 const int s = base + u * kChunk + 4 * lane;
+                const uint32_t vm = valid4(s, hi);
+                // bins above bin0: upper halves >= (bin0 + 1) << 4
+                above0 += (uint32_t)__popc(mask_gt4(h[u], (bin0 << 4) | 15u) & vm);
+                uint32_t d0[4];
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    if (s + j < hi) {
-                        const uint32_t d0 = h[u][j] >> 4;
-                        above0 += d0 > bin0 ? 1u : 0u;
-                        if (d0 == bin0) atomicAdd(&sh.hist[wave * 16 + (h[u][j] & 15u)], 1u);
-                    }
-                }
+                for (int j = 0; j < 4; ++j) d0[j] = h[u][j] >> 4;
+                const uint32_t inb = mask_eq4(d0, bin0) & vm;
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    if ((inb >> j) & 1u) atomicAdd(&sh.hist[wave * 16 + (h[u][j] & 15u)], 1u);
             }
         }
         above0 = wave_sum(above0);
@@ -431,35 +459,35 @@ __device__ __forceinline__ void topk_select(TopkShared& sh, const float* __restr
     // ---- gather the entries sharing the 16-bit prefix (when they fit)
     const bool gathered = in16 <= (uint32_t)kCandCap;
     if (gathered) {
-        constexpr int U = CACHED ? 4 : 8;
         for (int base = lo; base < hi; base += U * kChunk) {
             uint32_t h[U][4];
 #pragma unroll
-            for (int u = 0; u < U; ++u) hi4(base + u * kChunk + 4 * lane, h[u]);
+            for (int u = 0; u < U; ++u) {
+                if (base + u * kChunk < hi) {
+                    upper4<CACHED>(sh, row, base + u * kChunk, base + u * kChunk + 4 * lane, h[u]);
+                } else {
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) h[u][j] = 0;
+                }
+            }
 #pragma unroll
             for (int u = 0; u < U; ++u) {
                 const int s = base + u * kChunk + 4 * lane;
-                bool hit[4];
-                uint32_t total = 0, off = 0;
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    hit[j] = s + j < hi && h[u][j] == pre16;
-                    const uint64_t m = __ballot(hit[j]);
-                    total += (uint32_t)__popcll(m);
-                    off += (uint32_t)__popcll(m & below);
-                }
-                if (total) {  // wave-uniform
+                const uint32_t hit = mask_eq4(h[u], pre16) & valid4(s, hi);
+                if (__ballot(hit != 0u)) {  // wave-uniform
+                    uint32_t off, total;
+                    lane_prefix3((uint32_t)__popc(hit), off, total);
                     uint32_t at = 0;
                     if (lane == 0) at = atomicAdd(&sh.word[2], total);
-                    at = __shfl(at, 0) + off;
+                    at = (uint32_t)__builtin_amdgcn_readfirstlane((int)at) + off;
 #pragma unroll
                     for (int j = 0; j < 4; ++j)
-                        if (hit[j]) sh.cand_s[at++] = (uint32_t)(s + j);
+                        if ((hit >> j) & 1u) sh.cand_s[at++] = (uint32_t)(s + j);
                 }
             }
         }
         __syncthreads();
-        for (int i = tid; i < (int)in16; i += kTopkThreads) sh.cand_key[i] = float_key(src[sh.cand_s[i]]);
+        for (int i = tid; i < (int)in16; i += kTopkThreads) sh.cand_key[i] = row.key((int)sh.cand_s[i]);
         __syncthreads();
     }
 
@@ -476,7 +504,7 @@ __device__ __forceinline__ void topk_select(TopkShared& sh, const float* __restr
             }
         } else {
             for (int s = tid; s < n; s += kTopkThreads) {
-                const uint32_t u = float_key(src[s]);
+                const uint32_t u = row.key(s);
                 if ((u & mask) == prefix) atomicAdd(&sh.hist[(u >> shift) & 255], 1u);
             }
         }
@@ -507,8 +535,7 @@ __device__ __forceinline__ void topk_select(TopkShared& sh, const float* __restr
     const uint32_t thr = prefix;
 
     // ---- segment counts (and, for a cached row, flags) of the entries sharing pre16
-    const bool flags = CACHED && gathered;
-    if (flags)
+    if (CACHED && gathered)
         for (int i = tid; i < kBins0; i += kTopkThreads) sh.hist[i] = 0;
     __syncthreads();
     if (gathered) {
@@ -517,7 +544,7 @@ __device__ __forceinline__ void topk_select(TopkShared& sh, const float* __restr
             const int w = (int)s / seg;
             if (u > thr) atomicAdd(&sh.wgt[w], 1u);
             if (u == thr) atomicAdd(&sh.weq[w], 1u);
-            if (flags) {
+            if constexpr (CACHED) {
                 const uint32_t f = (u > thr ? 1u : 0u) | (u == thr ? 2u : 0u);
                 if (f) atomicOr(&sh.hist[s >> 4], f << (2 * (s & 15)));
             }
@@ -525,8 +552,8 @@ __device__ __forceinline__ void topk_select(TopkShared& sh, const float* __restr
     } else {
         uint32_t ng = 0, ne = 0;
         for (int s = lo + lane; s < hi; s += 64) {
-            const uint32_t u = float_key(src[s]);
-            ng += (u >> 16) == pre16 && u > thr ? 1u : 0u;
+            const uint32_t u = row.key(s);
+            ng += ((u >> 16) == pre16 && u > thr) ? 1u : 0u;
             ne += u == thr ? 1u : 0u;
         }
         ng = wave_sum(ng);
@@ -545,57 +572,61 @@ __device__ __forceinline__ void topk_select(TopkShared& sh, const float* __restr
         ties += sh.weq[w];
     }
     pos += min(ties, need);
-    constexpr int U = CACHED ? 4 : 8;
+    const bool flags = CACHED && gathered;
     for (int base = lo; base < hi; base += U * kChunk) {
-        uint32_t h[U][4];
+        uint32_t h[U][4], f8[U];
 #pragma unroll
-        for (int u = 0; u < U; ++u) hi4(base + u * kChunk + 4 * lane, h[u]);
+        for (int u = 0; u < U; ++u) {
+            f8[u] = 0;
+            if (base + u * kChunk < hi) {
+                const int s = base + u * kChunk + 4 * lane;
+                upper4<CACHED>(sh, row, base + u * kChunk, s, h[u]);
+                // flag bits of entries s .. s + 3: byte (s % 16) / 4 of flag word s / 16
+                if (flags) f8[u] = (sh.hist[s >> 4] >> (8 * (lane & 3))) & 0xffu;
+            } else {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) h[u][j] = 0;
+            }
+        }
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const int s = base + u * kChunk + 4 * lane;
-            bool gt[4], eq[4];
+            const uint32_t vm = valid4(s, hi);
+            const uint32_t mid = mask_eq4(h[u], pre16) & vm;  // share T's upper 16 bits
+            const uint32_t f = f8[u];
+            // de-interleave the flags: bit 2j = key > T, bit 2j + 1 = key == T
+            const uint32_t fgt = (f & 1u) | ((f >> 1) & 2u) | ((f >> 2) & 4u) | ((f >> 3) & 8u);
+            const uint32_t feq = ((f >> 1) & 1u) | ((f >> 2) & 2u) | ((f >> 3) & 4u) | ((f >> 4) & 8u);
+            uint32_t gtm = (mask_gt4(h[u], pre16) & vm) | (mid & fgt);
+            uint32_t eqm = mid & feq;
+            if (!flags && __ballot(mid != 0u)) {  // keys of the entries sharing pre16, from memory
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const bool valid = s + j < hi;
-                gt[j] = valid && h[u][j] > pre16;
-                eq[j] = false;
-                if (valid && h[u][j] == pre16) {
-                    if (flags) {
-                        const uint32_t f = sh.hist[(s + j) >> 4] >> (2 * ((s + j) & 15));
-                        gt[j] = f & 1u;
-                        eq[j] = (f >> 1) & 1u;
-                    } else {
-                        const uint32_t key = float_key(src[s + j]);
-                        gt[j] = key > thr;
-                        eq[j] = key == thr;
+                for (int j = 0; j < 4; ++j) {
+                    const uint32_t key = row.key(s + j);
+                    const uint32_t bit = mid & (1u << j);
+                    gtm |= key > thr ? bit : 0u;
+                    eqm |= key == thr ? bit : 0u;
+                }
+            }
+            uint32_t selm = gtm, tie_total = 0;
+            if (__ballot(eqm != 0u)) {  // rare: this step holds entries equal to T
+                uint32_t tie_off;
+                lane_prefix3((uint32_t)__popc(eqm), tie_off, tie_total);
+                uint32_t rank = ties + tie_off;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    if ((eqm >> j) & 1u) {
+                        if (rank < need) selm |= 1u << j;
+                        ++rank;
                     }
                 }
             }
-            uint32_t tie_off = 0, tie_total = 0;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const uint64_t m = __ballot(eq[j]);
-                tie_off += (uint32_t)__popcll(m & below);
-                tie_total += (uint32_t)__popcll(m);
-            }
-            bool sel[4];
-            uint32_t rank = ties + tie_off;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                sel[j] = gt[j] || (eq[j] && rank < need);
-                rank += eq[j] ? 1u : 0u;
-            }
-            uint32_t sel_off = 0, sel_total = 0;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const uint64_t m = __ballot(sel[j]);
-                sel_off += (uint32_t)__popcll(m & below);
-                sel_total += (uint32_t)__popcll(m);
-            }
+            uint32_t sel_off, sel_total;
+            lane_prefix3((uint32_t)__popc(selm), sel_off, sel_total);
             uint32_t at = pos + sel_off;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                if (sel[j]) {
+                if ((selm >> j) & 1u) {
                     if (at < (uint32_t)K) dst[at] = s + j;
                     ++at;
                 }
@@ -610,32 +641,41 @@ __global__ __launch_bounds__(kTopkThreads, 1) void indexer_topk_kernel(const flo
                                                                       const int32_t* __restrict__ len,
                                                                       int32_t* __restrict__ out, int L, int K) {
     __shared__ TopkShared sh;
-    const int row = blockIdx.x;
-    const int n = min(max(len[row], 0), L);
-    const float* src = logits + (int64_t)row * L;
-    int32_t* dst = out + (int64_t)row * K;
+    const int r = blockIdx.x;
+    const int n = min(max(len[r], 0), L);
+    int32_t* dst = out + (int64_t)r * K;
     if (n <= K) {  // every candidate is selected
         for (int j = threadIdx.x; j < K; j += kTopkThreads) dst[j] = j < n ? j : -1;
         return;
     }
-    const bool aligned = (reinterpret_cast<uintptr_t>(src) & 15) == 0;
+    const Row row{__builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(logits + (int64_t)r * L), (short)0, n * 4,
+                                                    0x00020000)};
     if (n <= kCacheKeys)
-        topk_select<true>(sh, src, dst, n, K, aligned);
+        topk_select<true>(sh, row, dst, n, K);
     else
-        topk_select<false>(sh, src, dst, n, K, aligned);
+        topk_select<false>(sh, row, dst, n, K);
+}
+
+template <int HI, int KS>
+int launch_logits(const IndexerParams& p, dim3 grid, hipStream_t stream) {
+    hipLaunchKernelGGL((indexer_logits_kernel<HI, KS>), grid, dim3(256), 0, stream, p);
+    return (int)hipGetLastError();
 }
 
 }  // namespace
 
 int launch_indexer_logits(const IndexerParams& p, hipStream_t stream) {
     const dim3 grid((unsigned)(p.B * p.tgroups), (unsigned)((p.ntiles + p.tiles_per_wg - 1) / p.tiles_per_wg));
-    if (p.HI == 64)
-        hipLaunchKernelGGL(indexer_logits_kernel<64>, grid, dim3(256), 0, stream, p);
-    else if (p.HI == 32)
-        hipLaunchKernelGGL(indexer_logits_kernel<32>, grid, dim3(256), 0, stream, p);
-    else
-        return (int)hipErrorInvalidValue;
-    return (int)hipGetLastError();
+    if (p.HI == 64) {
+        if (p.ks == 1) return launch_logits<64, 1>(p, grid, stream);
+        if (p.ks == 2) return launch_logits<64, 2>(p, grid, stream);
+        if (p.ks == 4) return launch_logits<64, 4>(p, grid, stream);
+    } else if (p.HI == 32) {
+        if (p.ks == 1) return launch_logits<32, 1>(p, grid, stream);
+        if (p.ks == 2) return launch_logits<32, 2>(p, grid, stream);
+        if (p.ks == 4) return launch_logits<32, 4>(p, grid, stream);
+    }
+    return (int)hipErrorInvalidValue;
 }
 
 int launch_indexer_topk(const float* logits, const int32_t* len, int32_t* indices, int rows, int L, int topk,

@@ -63,12 +63,13 @@ struct IndexerParams {
     const int32_t* len;      // [B, SQ] candidate keys per query (keys [0, len) are candidates)
     float* logits;           // [B, SQ, L] fp32; defined for s < len
     int B, SQ, HI, L;
-    int tgroups;             // query groups per batch: ceil(SQ / (256 / HI))
-    int ntiles;              // ceil(L / 64) key tiles
-    int tiles_per_wg;        // key tiles per workgroup
+    int ks;                  // waves sharing a query, splitting each key stage (1, 2, 4)
+    int tgroups;             // query groups per batch: ceil(SQ / (256 / HI / ks))
+    int ntiles;              // key stages: ceil(L / (64 * ks))
+    int tiles_per_wg;        // key stages per workgroup
 };
 
-// Enqueue the logits kernel (HI = 32 or 64); returns a hipError_t.
+// Enqueue the logits kernel (HI = 32 or 64, ks = 1, 2, 4); returns a hipError_t.
 int launch_indexer_logits(const IndexerParams& p, hipStream_t stream);
 
 // Enqueue the top-k selection: per row, the TOPK keys of largest logit among

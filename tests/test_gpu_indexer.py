@@ -54,6 +54,9 @@ LOGIT_CASES = [
     ("mtp h32", 1, 3, 2, 32, 3000, None),
     ("prefill causal h64", 2, 1, 300, 64, 1024, "causal"),
     ("lengths 0 and > L", 3, 2, 5, 64, 700, "edge"),
+    ("mtp h64", 4, 3, 2, 64, 4500, None),      # two waves per query (SQ * HI = 128)
+    ("sq3 h32", 5, 2, 3, 32, 2100, None),      # two waves per query, one slot idle
+    ("decode h32", 6, 5, 1, 32, 1500, None),   # four waves per query
 ]
 
 
