@@ -27,7 +27,12 @@ Functions and the reference code each one restates:
 
 * ``indexer_logits_ref`` / ``indexer_topk_ref`` / ``float_key`` -- the
                          lightning indexer (no reference counterpart: the
-                         reference takes the indices as an input).
+                         reference takes the indices as an input,
+                         README.md:19-21).  The logits restate the published
+                         DSA indexer score I[t,s] = sum_j w[t,j] *
+                         ReLU(q[t,j] . k[s]) (DeepSeek-V3.2-Exp report, eq. 1);
+                         the selection keeps the TOPK largest (ties: lower s)
+                         in ascending s, -1 padded.
 
 ``reference(scale=...)`` generalises the fixed 1/24 (tools/review.py:140) to
 another softmax scale; the default keeps the reference's exact division.
@@ -38,6 +43,9 @@ scaled_dot_product_attention (which also pins ``scale``), FP64 brute force,
 closed forms of the uniform family, index-permutation / -1-removal /
 duplicate-counting invariants, an identity block table and a gather
 restatement for ``unpage``, and planted mistakes that each check must reject.
+Indexer: FP64 brute-force logits (planted: ReLU or head weights dropped),
+brute-force selection over tie-heavy rows, -0.0 / +0.0, -inf and short rows
+(planted: ties taken from the top), and the float-key order.
 """
 from __future__ import annotations
 
