@@ -17,6 +17,9 @@ are timed the same way (K launches each), which gives the main kernel's
 average duration for the roofline.  An event between every launch would add
 its own few microseconds to each interval, so none is recorded inside a
 batch.  ``ms_per_step`` is the host wall clock of the K timed calls.
+``breakdown.kernel_sum_us`` adds the two kernels' launch-alone durations, and
+``breakdown.eager_call_us`` is the median wall clock of one ``dsa_amd.forward``
+call (checks, allocation, launches) followed by a device synchronisation.
 
 cpu_baseline: the CPU oracle (oracle/dsa_oracle.py, a restatement of the
 reference's FP32 PyTorch gather+softmax path) timed on this host on a bounded
@@ -153,6 +156,33 @@ def time_calls(calls, steps, warmup):
     return wall, main, merge, span
 
 
+def cpu_model():
+    """The host CPU's model name (/proc/cpuinfo), for the baseline record."""
+    try:
+        for ln in Path("/proc/cpuinfo").read_text().splitlines():
+            if ln.startswith("model name"):
+                return ln.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
+
+
+def eager_us(data, config, samples=30):
+    """Median wall clock of one dsa_amd.forward call (Python checks, output
+    allocation, launches) followed by a device synchronisation."""
+    q, kv, qr, kr, ids = data
+    for _ in range(3):
+        dsa_amd.forward(q, kv, qr, kr, ids, config=config)
+    torch.cuda.synchronize()
+    times = []
+    for _ in range(samples):
+        t0 = time.perf_counter()
+        dsa_amd.forward(q, kv, qr, kr, ids, config=config)
+        torch.cuda.synchronize()
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times) * 1e6
+
+
 def cpu_baseline(name, data, budget_s=10.0):
     """Time the CPU oracle on a bounded sample; scale to µs per full call."""
     from oracle import dsa_oracle as oracle
@@ -179,7 +209,7 @@ def cpu_baseline(name, data, budget_s=10.0):
             break
     per_call_us = statistics.median(times) * 1e6 * len(tokens) / len(sample)
     return {"value": round(per_call_us, 1), "unit": "µs/call", "cores": torch.get_num_threads(),
-            "kind": "port",
+            "kind": "port", "cpu": cpu_model(),
             "sample": (f"FP32 torch gather+softmax oracle on {len(sample)} of {len(tokens)} tokens of one "
                        f"{name} call, median of {len(times)} runs, scaled to a full call")}
 
@@ -263,8 +293,10 @@ def run(name, args):
             "span_us": round(span_us, 3),
             "main_us": round(main_us, 3),
             "merge_us": round(merge_us, 3),
+            "kernel_sum_us": round(main_us + merge_us, 3),
             "warm_span_us": round(warm_span, 3),
             "warm_main_us": round(warm_main, 3),
+            "eager_call_us": round(eager_us(sets[0], config), 2) if not args.paged else None,
             "gathered_TBps_main": round(gbytes / (main_us * 1e-6) / 1e12, 3),
             "mfma_TFLOPs_main": round(flops / (main_us * 1e-6) / 1e12, 2),
             "gathered_TBps_span": round(gbytes / (span_us * 1e-6) / 1e12, 3),
@@ -352,7 +384,7 @@ def indexer_cpu_baseline(name, data, budget_s=10.0):
             break
     per_call_us = statistics.median(times) * 1e6 * pairs_all / pairs_sample
     return {"value": round(per_call_us, 1), "unit": "µs/call", "cores": torch.get_num_threads(),
-            "kind": "port",
+            "kind": "port", "cpu": cpu_model(),
             "sample": (f"FP32 torch indexer logits + numpy top-k oracle on {len(rows)} of {batch * queries} "
                        f"queries of one {name} call, median of {len(times)} runs, scaled by (query, key) pairs")}
 
