@@ -156,9 +156,12 @@ __device__ __forceinline__ void gather_lanes(uint32_t lds_base, rsrc_t rsrc, uin
 // chunks); logical chunk c of tile row r lives at physical chunk c ^ sw_kv(r)
 // (only the low 4 bits move).  sw_kv is a permutation of 0..15 whose values
 // differ in bits [3:2] within every group of 4 consecutive rows and in bits
-// [3:1] within every group of 8, which makes the QK reads (16 rows x 16 B per
-// quarter-wave) and the transposed PV reads of both variants bank-conflict
-// free.  A rope row occupies 128 bytes (8 chunks): physical = c ^ sw_rope(r).
+// [3:1] within every group of 8.  LDS has 64 banks (a 256-byte period); a
+// ds_read_b128 serves 16 lanes per pass, four quads of lanes: quad q of a
+// half-wave (lanes 4q..4q+3) joins pass parity(popcount(q)).  With the QK
+// chunk assignment of each variant and the transposed PV reads, every pass
+// touches 16 distinct bank groups (rocprofv3 SQ_LDS_BANK_CONFLICT reads 0).
+// A rope row occupies 128 bytes (8 chunks): physical = c ^ sw_rope(r).
 __device__ __forceinline__ int sw_kv(int r) {
     return ((r & 3) << 2) | (((r >> 2) & 1) << 1) | ((r >> 3) & 1);  // uses r mod 16
 }
@@ -685,17 +688,26 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd_narrow(FwdParams p
 
     const WgCoords c = wg_coords<kBN>(p);
     const int head = c.hgi * (16 * HW) + hw * 16 + n16;  // this lane's head
+    // QK k-step ks (ks < 16) gives k-group g the 16-byte chunk 16 g + ks of the
+    // 512 latent dims (Q and K agree; a dot product does not depend on the
+    // order of its terms), so each k-group reads its own 256-byte window of
+    // the row.  A ds_read_b128 serves the lanes 16 at a time, in quads: quad
+    // q of a half-wave joins pass parity(popcount(q)) (measured on gfx950), so
+    // a pass holds k-groups 0 and 1 (or 2 and 3) over complementary sets of 8
+    // rows; with one window per k-group its 16 chunks are ks ^ sw_kv(row)
+    // over all 16 rows -- 16 distinct bank groups.
 
     // Index loads first: the first gather depends on them, Q only on the
     // first MFMA.
     const IdxRegs ids = fetch_indices<kBN>(p, c);
 
-    // ---- Q fragments: lane holds Q[head][32*ks + 8*g .. +7]; ks 16, 17 from q_rope.
+    // ---- Q fragments: lane holds Q[head][128*g + 8*ks .. +7]; ks 16, 17 from
+    // q_rope (dims 32*(ks-16) + 8*g).
     bf16x8 qf[18];
     {
-        const uint16_t* qrow = p.q + ((int64_t)c.token * p.H + head) * 512 + 8 * g;
+        const uint16_t* qrow = p.q + ((int64_t)c.token * p.H + head) * 512 + 128 * g;
 #pragma unroll
-        for (int ks = 0; ks < 16; ++ks) qf[ks] = *reinterpret_cast<const bf16x8*>(qrow + 32 * ks);
+        for (int ks = 0; ks < 16; ++ks) qf[ks] = *reinterpret_cast<const bf16x8*>(qrow + 8 * ks);
         const uint16_t* rrow = p.q_rope + ((int64_t)c.token * p.H + head) * 64 + 8 * g;
         qf[16] = *reinterpret_cast<const bf16x8*>(rrow);
         qf[17] = *reinterpret_cast<const bf16x8*>(rrow + 32);
@@ -708,10 +720,10 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd_narrow(FwdParams p
 
     // ---- per-lane LDS offsets (see the wide variant).
     const int rowbase = kw * RPW;
-    // QK A operand: row rowbase + 16*s + n16, logical chunk 4*ks + g = 16*(ks>>2) + (4*(ks&3) + g)
-    uint32_t qk_off[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) qk_off[j] = ((4 * j + g) ^ sw_kv(n16)) << 4;
+    // QK A operand: row rowbase + 16*s + n16, logical chunk 16*g + ks at byte
+    // 256*g + ((ks ^ sw_kv(n16)) << 4) of the row.
+    const uint32_t qk_g = (uint32_t)g << 8;
+    const uint32_t qk_x = (uint32_t)sw_kv(n16) << 4;
     uint32_t rp_off[2];
 #pragma unroll
     for (int j = 0; j < 2; ++j) rp_off[j] = ((4 * j + g) ^ sw_rope(n16)) << 4;
@@ -765,7 +777,7 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd_narrow(FwdParams p
         auto kfrag = [&](int step) -> bf16x8 {
             const int ks = step / NSUB, s = step % NSUB;
             const int row = rowbase + 16 * s + n16;
-            return ks < 16 ? lds_load<bf16x8>(stage + row * 1024 + qk_off[ks & 3] + ((ks >> 2) << 8))
+            return ks < 16 ? lds_load<bf16x8>(stage + row * 1024 + qk_g + ((uint32_t)(16 * ks) ^ qk_x))
                            : lds_load<bf16x8>(stage + R::KV_BYTES + row * 128 + rp_off[ks - 16]);
         };
         {
@@ -904,9 +916,13 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd_narrow(FwdParams p
             lds_store<float>(ml + 4 * (kWaves * 16 + wave * 16 + n16), m_true);
             lds_store<float>(ml + 4 * (2 * kWaves * 16 + wave * 16 + n16), l_run);
         }
-        const uint32_t ox = lds + ((wave * 16 + n16) * OX_STRIDE + 4 * g) * 4;
+        // Head row (wave, n16): column group g of block cb at float 128 g + 4 cb,
+        // so a lane's bank group is set by its row alone (rows are 129 chunks
+        // apart) and each 16-lane pass of ds_write/read_b128 -- k-groups 0 and 1
+        // over complementary rows -- touches 16 distinct bank groups.
+        const uint32_t ox = lds + ((wave * 16 + n16) * OX_STRIDE + 128 * g) * 4;
 #pragma unroll
-        for (int cb = 0; cb < 32; ++cb) lds_store<f32x4>(ox + cb * 64, oacc[cb]);
+        for (int cb = 0; cb < 32; ++cb) lds_store<f32x4>(ox + cb * 16, oacc[cb]);
         lds_barrier();
         float mk[KW], lk[KW];
         float mref = -FLT_MAX, mtrue = -FLT_MAX;
@@ -938,7 +954,7 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd_narrow(FwdParams p
 #pragma unroll
                 for (int k = 0; k < KW; ++k) {
                     const int wk = k * HW + hw;
-                    const f32x4 v = lds_load<f32x4>(lds + ((wk * 16 + n16) * OX_STRIDE + 4 * g + cb * 16) * 4);
+                    const f32x4 v = lds_load<f32x4>(lds + ((wk * 16 + n16) * OX_STRIDE + 128 * g + 4 * cb) * 4);
                     acc += wgt[k] * v;
                 }
                 oacc[cb] = acc;
