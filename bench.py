@@ -63,17 +63,18 @@ DEFAULT_ROTATE = {"c1_decode_b1": 16, "c2_decode_b8": 32, "c3_decode_h16_mtp": 2
                   "c4_prefill_h16": 1, "c5_prefill_h128": 1}
 
 
-def algorithmic_units(shape):
+def algorithmic_units(shape, fp8=False):
     """Gathered bytes and FLOPs of one call: every slot counted once
-    (B*SQ*TOPK rows of 576 bf16) and 2*B*SQ*H*TOPK*(576+512) MFMA FLOPs."""
+    (B*SQ*TOPK rows of 576 bf16, or of 656 bytes in the fp8 row format) and
+    2*B*SQ*H*TOPK*(576+512) MFMA FLOPs."""
     b, sq, h, _, k = shape
-    return b * sq * k * 576 * 2, 2 * b * sq * h * k * (576 + 512)
+    return b * sq * k * (656 if fp8 else 576 * 2), 2 * b * sq * h * k * (576 + 512)
 
 
 class Call:
     """One preallocated forward call through the C ABI."""
 
-    def __init__(self, data, config: Tuning, block_table=None):
+    def __init__(self, data, config: Tuning, block_table=None, fp8=False):
         self.data = data
         q = data[0]
         length = data[1].shape[1] if block_table is None else block_table.shape[1] * data[1].shape[1]
@@ -83,6 +84,10 @@ class Call:
             self.block_table = block_table
             self.opts = _lib.DsaFwdOptions(block_size=data[1].shape[1], max_blocks=block_table.shape[1],
                                            num_blocks=data[1].shape[0], block_table=block_table.data_ptr())
+        if fp8:  # data[1] holds 656-byte rows, data[3] is None
+            if self.opts is None:
+                self.opts = _lib.DsaFwdOptions()
+            self.opts.kv_format = _lib.KV_FP8
         b, sq, h, _, _ = self.shape
         self.config = config
         self.plan = config.to_c()
@@ -187,7 +192,12 @@ def cpu_baseline(name, data, budget_s=10.0):
     """Time the CPU oracle on a bounded sample; scale to µs per full call."""
     from oracle import dsa_oracle as oracle
 
-    q, kv, qr, kr, ids = (t.cpu() for t in data)
+    fp8 = data[3] is None  # kv holds fp8 rows: the oracle runs on their dequantized values
+    if fp8:
+        kv, kr = oracle.dequant_fp8_rows(data[1])
+        q, qr, ids = (t.cpu() for t in (data[0], data[2], data[4]))
+    else:
+        q, kv, qr, kr, ids = (t.cpu() for t in data)
     batch, queries = q.shape[:2]
     tokens = [(b, s) for b in range(batch) for s in range(queries)]
     # sample: whole call when small, else an evenly spaced token subset
@@ -211,7 +221,8 @@ def cpu_baseline(name, data, budget_s=10.0):
     return {"value": round(per_call_us, 1), "unit": "µs/call", "cores": torch.get_num_threads(),
             "kind": "port", "cpu": cpu_model(),
             "sample": (f"FP32 torch gather+softmax oracle on {len(sample)} of {len(tokens)} tokens of one "
-                       f"{name} call, median of {len(times)} runs, scaled to a full call")}
+                       f"{name} call, median of {len(times)} runs, scaled to a full call"
+                       + ("; kv dequantized from the fp8 rows beforehand (not timed)" if fp8 else ""))}
 
 
 def traffic_from_profiles(name):
@@ -243,7 +254,7 @@ def paged(data, block_size, seed):
 def run(name, args):
     shape = BASELINE_CONFIGS[name]
     rotate = args.rotate if args.rotate else DEFAULT_ROTATE[name]
-    config = dsa_amd.select(shape)
+    config = dsa_amd.select(shape, kv_fp8=args.fp8)
     if args.plan:
         v = [int(x) for x in args.plan.split(",")]
         bm, split, kv_waves, mfma = v[:4]
@@ -251,6 +262,10 @@ def run(name, args):
         config = Tuning(bm, bn, split, kv_waves=kv_waves, stages=stages, mfma=mfma)
     print(f"[bench] {name} shape={shape} plan={config} rotate={rotate}", file=sys.stderr, flush=True)
     sets = [baseline_inputs(name, seed=args.seed + i, device="cuda", cpu_recipe=False) for i in range(rotate)]
+    if args.fp8:  # the same inputs with kv and k_rope written as 656-byte fp8 rows
+        for i, d in enumerate(sets):
+            sets[i] = (d[0], dsa_amd.quantize_kv_fp8(d[1], d[3]), d[2], None, d[4])
+        torch.cuda.synchronize()
     if args.paged:
         calls = []
         for i, d in enumerate(sets):
@@ -259,10 +274,10 @@ def run(name, args):
             if i:  # set 0 stays for the CPU baseline
                 sets[i] = None
     else:
-        calls = [Call(d, config) for d in sets]
+        calls = [Call(d, config, fp8=args.fp8) for d in sets]
     wall, main_us, merge_us, span_us = time_calls(calls, args.steps, args.warmup)
     _, warm_main, _, warm_span = time_calls(calls[:1], args.steps, args.warmup)
-    gbytes, flops = algorithmic_units(shape)
+    gbytes, flops = algorithmic_units(shape, args.fp8)
     bound = BOUND[name]
     if bound == "hbm":
         achieved, peak, unit = gbytes / (main_us * 1e-6) / 1e9, HBM_PEAK_GBS, "GB/s"
@@ -282,13 +297,17 @@ def run(name, args):
         "dtype": "bf16",
         "data": (f"synthetic: seeded N(0,1) bf16 q/kv/rope, per-workload index recipe, "
                  f"{rotate} rotating input set(s) resident in HBM"
-                 + (f"; kv paged in {args.paged}-row blocks under a random block table" if args.paged else "")),
+                 + (f"; kv paged in {args.paged}-row blocks under a random block table" if args.paged else "")
+                 + ("; kv cache as 656-byte fp8 rows (e4m3 latent, fp32 block scales, bf16 rope)"
+                    if args.fp8 else "")),
         "config": {"workload": name, "B": shape[0], "SQ": shape[1], "H": shape[2], "L": shape[3],
                    "TOPK": shape[4], "plan": vars(config) if hasattr(config, "__dict__") else str(config),
-                   "rotating_input_sets": rotate, "paged_block_size": args.paged or None},
+                   "rotating_input_sets": rotate, "paged_block_size": args.paged or None,
+                   "kv_format": "fp8" if args.fp8 else "bf16"},
         "roofline": {"bound": bound, "achieved": round(achieved, 2), "peak": peak, "unit": unit,
                      "frac": round(achieved / peak, 4), "traffic": traffic_from_profiles(name),
                      "kernel": f"sparse_mla_fwd (main), {gbytes} gathered B and {flops} FLOP per launch"},
+        **({"dtype_note": "kv stored as fp8 e4m3 rows; MFMA inputs bf16"} if args.fp8 else {}),
         "breakdown": {
             "span_us": round(span_us, 3),
             "main_us": round(main_us, 3),
@@ -296,7 +315,7 @@ def run(name, args):
             "kernel_sum_us": round(main_us + merge_us, 3),
             "warm_span_us": round(warm_span, 3),
             "warm_main_us": round(warm_main, 3),
-            "eager_call_us": round(eager_us(sets[0], config), 2) if not args.paged else None,
+            "eager_call_us": round(eager_us(sets[0], config), 2) if not args.paged and not args.fp8 else None,
             "gathered_TBps_main": round(gbytes / (main_us * 1e-6) / 1e12, 3),
             "mfma_TFLOPs_main": round(flops / (main_us * 1e-6) / 1e12, 2),
             "gathered_TBps_span": round(gbytes / (span_us * 1e-6) / 1e12, 3),
@@ -453,6 +472,8 @@ def main():
     ap.add_argument("--seed", type=int, default=20261102)
     ap.add_argument("--paged", type=int, default=0, metavar="BLOCK",
                     help="run the workload on paged kv (block pools of BLOCK rows, random block table)")
+    ap.add_argument("--fp8", action="store_true",
+                    help="run the workload on the fp8 kv row format (656 bytes per row)")
     ap.add_argument("--indexer", default="", metavar="WORKLOAD",
                     help="time the lightning indexer instead: " + ", ".join(INDEXER_CONFIGS) + " or all")
     ap.add_argument("--no-cpu-baseline", action="store_true")

@@ -39,14 +39,22 @@ class DsaFwdOptions(ctypes.Structure):
         ("max_blocks", ctypes.c_int32),
         ("num_blocks", ctypes.c_int32),
         ("block_table", ctypes.c_void_p),
-        ("reserved", ctypes.c_int64 * 2),
+        ("kv_format", ctypes.c_int32),
+        ("reserved32", ctypes.c_int32),
+        ("reserved", ctypes.c_int64 * 1),
     ]
+
+
+KV_BF16 = 0  # DSA_KV_BF16
+KV_FP8 = 1   # DSA_KV_FP8: 656-byte rows (512 e4m3, 4 fp32 scales, 64 bf16 rope)
 
 
 SIGNATURES = {
     "dsa_version": (_i32, []),
     "dsa_last_error": (ctypes.c_char_p, []),
     "dsa_plan_for": (_i32, [_i32, _i32, _i32, _i32, _i32, _i32, ctypes.POINTER(DsaPlan)]),
+    "dsa_plan_for_opts": (_i32, [_i32, _i32, _i32, _i32, _i32, _i32, ctypes.POINTER(DsaFwdOptions),
+                                 ctypes.POINTER(DsaPlan)]),
     "dsa_plan_check": (_i32, [ctypes.POINTER(DsaPlan), _i32, _i32, _i32, _i32, _i32]),
     "dsa_partial_elems": (_i32, [ctypes.POINTER(DsaPlan), _i32, _i32, _i32,
                                  ctypes.POINTER(_i64), ctypes.POINTER(_i64)]),

@@ -19,6 +19,7 @@ from .config import Tuning, check_tuning, select
 
 HEAD_DIM = 512
 ROPE_DIM = 64
+FP8_ROW = 656  # bytes of an fp8 kv row: 512 e4m3 latent values, 4 fp32 scales, 64 bf16 rope values
 SCALE = 1.0 / 24.0  # 576 ** -0.5, the reference's fixed scale (README.md:81-83 of the reference)
 _LDS_BYTES = 2 * 64 * 1152 + 2048 * 4
 
@@ -41,8 +42,15 @@ def _check_inputs(q, kv, q_rope, k_rope, indices, block_table=None):
     ``block_table`` (paged kv, no reference counterpart) kv and k_rope are
     block pools ``[num_blocks, block_size, 1, 512 / 64]``, ``block_table`` is
     int32 ``[B, max_blocks]`` and the logical length is
-    ``L = max_blocks * block_size``.
+    ``L = max_blocks * block_size``.  A uint8 ``kv`` whose last dim is 656
+    holds fp8 rows (no reference counterpart; ``k_rope`` must then be None).
+    Returns ``(shape, device, fp8)``.
     """
+    fp8 = kv.dtype == torch.uint8 and kv.dim() == 4 and kv.shape[-1] == FP8_ROW
+    if fp8 and k_rope is not None:
+        raise ValueError("with fp8 kv rows (uint8 [..., 656]) k_rope must be None: the rope values are in the rows")
+    if not fp8 and k_rope is None:
+        raise ValueError("k_rope is required unless kv holds fp8 rows (uint8 [..., 656])")
     q_shape, kv_shape, ids_shape = tuple(q.shape), tuple(kv.shape), tuple(indices.shape)
     if len(q_shape) != 4 or len(kv_shape) != 4 or len(ids_shape) != 4:
         raise ValueError("q, kv and indices must be 4-D tensors")
@@ -56,11 +64,14 @@ def _check_inputs(q, kv, q_rope, k_rope, indices, block_table=None):
             raise ValueError("block_table must be [B, max_blocks]")
         pool = kv_shape[:2]
         length = block_table.shape[1] * kv_shape[1]
-    if (width != HEAD_DIM or kv_shape != (*pool, 1, HEAD_DIM)
+    if (width != HEAD_DIM or kv_shape != (*pool, 1, FP8_ROW if fp8 else HEAD_DIM)
             or tuple(q_rope.shape) != (batch, queries, heads, ROPE_DIM)
-            or tuple(k_rope.shape) != (*pool, 1, ROPE_DIM)
+            or (not fp8 and tuple(k_rope.shape) != (*pool, 1, ROPE_DIM))
             or ids_shape != (batch, queries, 1, topk)
             or min(batch, queries, heads, length, topk, *pool) <= 0):
+        if fp8:
+            raise ValueError("expected q[B,SQ,H,512], kv fp8 rows [B,L,1,656] (or a [N,BS,1,656] pool), "
+                             "q_rope[B,SQ,H,64], indices[B,SQ,1,K]")
         if block_table is None:
             raise ValueError("expected q[B,SQ,H,512], kv[B,L,1,512], q_rope[B,SQ,H,64], "
                              "k_rope[B,L,1,64], indices[B,SQ,1,K]")
@@ -69,17 +80,18 @@ def _check_inputs(q, kv, q_rope, k_rope, indices, block_table=None):
     if heads % 16:
         raise ValueError(f"the number of heads must be a multiple of 16 (got {heads})")
     device = q.device
-    tensors = (kv, q_rope, k_rope, indices) + (() if block_table is None else (block_table,))
+    tensors = (kv, q_rope) + (() if fp8 else (k_rope,)) + (indices,) + (() if block_table is None else (block_table,))
     if (device.type != "cuda" or torch.version.hip is None
             or any(t.device != device for t in tensors)
             or not all(t.is_contiguous() for t in (q,) + tensors)):
         raise ValueError("all inputs must be contiguous and on the same ROCm GPU")
     bf16 = torch.bfloat16
-    if (q.dtype != bf16 or kv.dtype != bf16 or q_rope.dtype != bf16 or k_rope.dtype != bf16
+    if (q.dtype != bf16 or (not fp8 and kv.dtype != bf16) or q_rope.dtype != bf16
+            or (not fp8 and k_rope.dtype != bf16)
             or indices.dtype != torch.int32
             or (block_table is not None and block_table.dtype != torch.int32)):
         raise ValueError("q/kv/q_rope/k_rope must be bfloat16 and indices (and block_table) int32")
-    return (batch, queries, heads, length, topk), device
+    return (batch, queries, heads, length, topk), device, fp8
 
 
 def _check_scale(scale):
@@ -93,17 +105,21 @@ def _check_scale(scale):
     return scale
 
 
-def plan_call(shape, config=None, cores: int = 256):
+def plan_call(shape, config=None, cores: int = 256, kv_fp8: bool = False):
     """Plan of one call: (Tuning, partial-buffer shapes or None, launches).
 
     Pure host logic (reference: dsa/api.py:88-113); usable without a GPU.
+    ``kv_fp8``: the call reads fp8 kv rows, which only the narrow variants
+    (``mfma=16``) do.
     """
     if type(cores) is not int or cores <= 0:
         raise ValueError("cores must be a positive int")
     if config is None:
-        config = select(shape, cores)
+        config = select(shape, cores, kv_fp8)
     else:
         check_tuning(config, shape)
+        if kv_fp8 and config.mfma != 16:
+            raise ValueError("fp8 kv rows need a narrow plan (mfma=16)")
     batch, queries, heads, _, _ = shape
     tokens = batch * queries
     variant = "wide" if config.mfma == 32 else "narrow"
@@ -137,13 +153,16 @@ def forward(q, kv, q_rope, k_rope, indices, *, config=None, cores=None, return_k
     and k_rope given as block pools ``[num_blocks, block_size, 1, 512 / 64]``;
     logical row ``I`` of batch ``b`` is pool row
     ``block_table[b, I // block_size] * block_size + I % block_size`` and a
-    slot whose block entry is outside ``[0, num_blocks)`` is masked.
+    slot whose block entry is outside ``[0, num_blocks)`` is masked.  An fp8
+    kv cache is a uint8 ``kv [B, L, 1, 656]`` (or pool) of rows written by
+    :func:`dsa_amd.quantize_kv_fp8`, with ``k_rope=None``; the kernel computes
+    with ``bf16(fp32(e4m3) * scale)`` latent values.
     """
     scale = _check_scale(scale)
-    shape, device = _check_inputs(q, kv, q_rope, k_rope, indices, block_table)
+    shape, device, fp8 = _check_inputs(q, kv, q_rope, k_rope, indices, block_table)
     if cores is None:
         cores = torch.cuda.get_device_properties(device).multi_processor_count
-    config, partials, launches = plan_call(shape, config, cores)
+    config, partials, launches = plan_call(shape, config, cores, fp8)
     batch, queries, heads, length, topk = shape
 
     output = torch.empty_like(q)
@@ -165,11 +184,12 @@ def forward(q, kv, q_rope, k_rope, indices, *, config=None, cores=None, return_k
             ptr(output), ptr(maximum), ptr(denominator), ptr(part_o), ptr(part_m), ptr(part_l),
             batch, queries, heads, length, topk)
     with torch.cuda.device(device):
-        if scale is None and block_table is None:
+        if scale is None and block_table is None and not fp8:
             rc = _lib.load().dsa_fwd(*args, ctypes.byref(plan), ctypes.c_void_p(stream))
         else:
             opts = _lib.DsaFwdOptions()
             opts.scale = 0.0 if scale is None else scale
+            opts.kv_format = _lib.KV_FP8 if fp8 else _lib.KV_BF16
             if block_table is not None:
                 opts.block_size = kv.shape[1]
                 opts.max_blocks = block_table.shape[1]

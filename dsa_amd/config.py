@@ -78,12 +78,17 @@ CASE_SHAPES = {
 MI355X_CUS = 256
 
 
-def plan_for(shape, num_cus: int = MI355X_CUS) -> Tuning:
-    """Default plan the library derives for ``shape`` on ``num_cus`` CUs."""
+def plan_for(shape, num_cus: int = MI355X_CUS, kv_fp8: bool = False) -> Tuning:
+    """Default plan the library derives for ``shape`` on ``num_cus`` CUs (with
+    ``kv_fp8``, among the variants that read 656-byte fp8 kv rows)."""
     b, sq, h, length, topk = shape
     out = _lib.DsaPlan()
-    _lib.check(_lib.load().dsa_plan_for(b, sq, h, length, topk, num_cus, ctypes.byref(out)),
-               "dsa_plan_for")
+    if kv_fp8:
+        opts = _lib.DsaFwdOptions(kv_format=_lib.KV_FP8)
+        rc = _lib.load().dsa_plan_for_opts(b, sq, h, length, topk, num_cus, ctypes.byref(opts), ctypes.byref(out))
+    else:
+        rc = _lib.load().dsa_plan_for(b, sq, h, length, topk, num_cus, ctypes.byref(out))
+    _lib.check(rc, "dsa_plan_for")
     return Tuning.from_c(out)
 
 
@@ -131,9 +136,10 @@ for _name, _shape in CASE_SHAPES.items():
     _BY_SHAPE.setdefault(_shape, SELECTED[_name])
 
 
-def select(shape, num_cus: int = MI355X_CUS) -> Tuning:
-    """Plan for a shape: the table entry on a 256-CU device, else the planner's."""
+def select(shape, num_cus: int = MI355X_CUS, kv_fp8: bool = False) -> Tuning:
+    """Plan for a shape: the table entry on a 256-CU device, else the planner's
+    (fp8 kv rows: always the planner's, which keeps to the narrow variants)."""
     shape = tuple(shape)
-    if num_cus == MI355X_CUS and shape in _BY_SHAPE:
+    if not kv_fp8 and num_cus == MI355X_CUS and shape in _BY_SHAPE:
         return _BY_SHAPE[shape]
-    return plan_for(shape, num_cus)
+    return plan_for(shape, num_cus, kv_fp8)

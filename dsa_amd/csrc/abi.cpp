@@ -75,7 +75,14 @@ int dsa_plan_check(const dsa_plan* plan, int B, int SQ, int H, int L, int TOPK) 
     return 0;
 }
 
-int dsa_plan_for(int B, int SQ, int H, int L, int TOPK, int num_cus, dsa_plan* out) {
+}  // extern "C"
+
+namespace {
+
+// The planner behind dsa_plan_for; `fp8` restricts it to the variants that
+// read 656-byte fp8 kv rows (the narrow ones) and prices their gathers and
+// per-tile expansion.
+int plan_impl(int B, int SQ, int H, int L, int TOPK, int num_cus, bool fp8, dsa_plan* out) {
     if (!out) return fail(-1, "out is NULL");
     if (int rc = check_shape(B, SQ, H, L, TOPK)) return rc;
     if (num_cus <= 0) return fail(-1, "num_cus must be positive (got %d)", num_cus);
@@ -101,12 +108,15 @@ int dsa_plan_for(int B, int SQ, int H, int L, int TOPK, int num_cus, dsa_plan* o
     constexpr double kClockMHz = 2200.0, kPrologueCycles = 9000.0, kLaunchUs = 2.0;
     constexpr double kHbmBytesPerUs = 4.8e6, kCuBytesPerUs = 3.0e4;                // sustained gather rates
     constexpr double kMergeUs = 2.0, kMergeWgBytesPerUs = 4.2e4, kMergeBytesPerUs = 6.0e6;
+    constexpr double kFp8TileCycles = 1200.0;  // expanding a 64-row fp8 tile to bf16 in LDS
     const int64_t tokens = (int64_t)B * SQ;
-    const double gathered = (double)tokens * TOPK * 1152.0;
+    const double gathered = (double)tokens * TOPK * (fp8 ? 656.0 : 1152.0);
     double best = -1.0;
     dsa_plan p{};
     for (const Variant& v : kVariants) {
         if (H % v.hpg) continue;
+        if (fp8 && v.mfma != 16) continue;
+        const double tile_cycles = v.tile_cycles + (fp8 ? kFp8TileCycles : 0.0);
         const int ntiles = ceil_div(TOPK, v.bn);
         const int min_split = ceil_div(ntiles * v.bn, DSA_IDX_CAP);
         const int64_t groups = tokens * (H / v.hpg);
@@ -115,7 +125,7 @@ int dsa_plan_for(int B, int SQ, int H, int L, int TOPK, int num_cus, dsa_plan* o
             if (wgs > 0x7fffffff) break;
             const double rounds = (double)((wgs + num_cus - 1) / num_cus);
             const double tiles = (double)ceil_div(ntiles, split);
-            const double wg_us = (kPrologueCycles + tiles * v.tile_cycles + v.epilogue_cycles) / kClockMHz;
+            const double wg_us = (kPrologueCycles + tiles * tile_cycles + v.epilogue_cycles) / kClockMHz;
             const double active = (double)(wgs < num_cus ? wgs : num_cus);
             const double hbm = active * kCuBytesPerUs < kHbmBytesPerUs ? active * kCuBytesPerUs : kHbmBytesPerUs;
             double main_us = rounds * wg_us;
@@ -139,6 +149,21 @@ int dsa_plan_for(int B, int SQ, int H, int L, int TOPK, int num_cus, dsa_plan* o
     if (best < 0.0) return fail(-1, "no kernel variant for H=%d", H);
     *out = p;
     return dsa_plan_check(out, B, SQ, H, L, TOPK);
+}
+
+}  // namespace
+
+extern "C" {
+
+int dsa_plan_for(int B, int SQ, int H, int L, int TOPK, int num_cus, dsa_plan* out) {
+    return plan_impl(B, SQ, H, L, TOPK, num_cus, false, out);
+}
+
+int dsa_plan_for_opts(int B, int SQ, int H, int L, int TOPK, int num_cus, const dsa_fwd_options* opts,
+                      dsa_plan* out) {
+    if (opts && opts->kv_format != DSA_KV_BF16 && opts->kv_format != DSA_KV_FP8)
+        return fail(-1, "kv_format must be DSA_KV_BF16 (0) or DSA_KV_FP8 (1) (got %d)", opts->kv_format);
+    return plan_impl(B, SQ, H, L, TOPK, num_cus, opts && opts->kv_format == DSA_KV_FP8, out);
 }
 
 int dsa_partial_elems(const dsa_plan* plan, int B, int SQ, int H, int64_t* part_o_elems,
@@ -173,7 +198,8 @@ int fwd_impl(const uint16_t* q, const uint16_t* kv, const uint16_t* q_rope, cons
              const int32_t* idx, uint16_t* out, float* out_max, float* out_sum, float* part_o, float* part_m,
              float* part_l, int B, int SQ, int H, int L, int TOPK, const dsa_fwd_options* opts,
              const dsa_plan* plan, hipStream_t stream, bool with_merge) {
-    if (!q || !kv || !q_rope || !k_rope || !idx) return fail(-1, "NULL input pointer");
+    const bool fp8 = opts && opts->kv_format == DSA_KV_FP8;
+    if (!q || !kv || !q_rope || (!k_rope && !fp8) || !idx) return fail(-1, "NULL input pointer");
     if (int rc = check_shape(B, SQ, H, L, TOPK)) return rc;
     // Options: scale in log2 units (the default is the reference's 1/24) and
     // the paged-kv geometry.
@@ -181,6 +207,9 @@ int fwd_impl(const uint16_t* q, const uint16_t* kv, const uint16_t* q_rope, cons
     const int32_t* block_table = nullptr;
     int block_size = 0, max_blocks = 0, kv_rows = L;
     if (opts) {
+        if (opts->kv_format != DSA_KV_BF16 && opts->kv_format != DSA_KV_FP8)
+            return fail(-1, "kv_format must be DSA_KV_BF16 (0) or DSA_KV_FP8 (1) (got %d)", opts->kv_format);
+        if (opts->reserved32 || opts->reserved[0]) return fail(-1, "reserved option fields must be zero");
         if (opts->scale != 0.0f) {
             if (!(opts->scale > 0.0f) || !std::isfinite(opts->scale))
                 return fail(-1, "scale must be a positive finite number (got %g)", (double)opts->scale);
@@ -209,18 +238,19 @@ int fwd_impl(const uint16_t* q, const uint16_t* kv, const uint16_t* q_rope, cons
         int err = (int)hipGetDevice(&dev);
         if (!err) err = (int)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
         if (err) return hip_fail(err, "querying the CU count");
-        if (int rc = dsa_plan_for(B, SQ, H, L, TOPK, cus, &local)) return rc;
+        if (int rc = plan_impl(B, SQ, H, L, TOPK, cus, fp8, &local)) return rc;
         plan = &local;
     } else if (int rc = dsa_plan_check(plan, B, SQ, H, L, TOPK)) {
         return rc;
     }
+    if (fp8 && plan->mfma != 16) return fail(-1, "fp8 kv rows need a narrow plan (mfma 16)");
     const bool split = plan->split > 1;
     if ((!split || with_merge) && (!out || !out_max || !out_sum)) return fail(-1, "NULL output pointer");
     if (split && (!part_o || !part_m || !part_l))
         return fail(-1, "split=%d needs part_o, part_m and part_l", plan->split);
     // 16-byte vector accesses need 16-byte aligned rows.
     if (((uintptr_t)q | (uintptr_t)kv | (uintptr_t)q_rope | (uintptr_t)k_rope) & 15)
-        return fail(-1, "q, kv, q_rope and k_rope must be 16-byte aligned");
+        return fail(-1, "q, kv, q_rope and k_rope must be 16-byte aligned");  // fp8 rows: 656 = 41 x 16
     if (out && ((uintptr_t)out & 15)) return fail(-1, "out must be 16-byte aligned");
     if (split && ((uintptr_t)part_o & 15)) return fail(-1, "part_o must be 16-byte aligned");
     const int64_t rowgroups = (int64_t)B * SQ * plan->split;
@@ -248,6 +278,7 @@ int fwd_impl(const uint16_t* q, const uint16_t* kv, const uint16_t* q_rope, cons
     p.block_size = block_size;
     p.max_blocks = max_blocks;
     p.kv_rows = kv_rows;
+    p.kv_fp8 = fp8 ? 1 : 0;
     p.nsplit = plan->split;
     p.ntiles = ceil_div(TOPK, plan->tile_rows);
     p.hgroups = H / plan->heads_per_group;

@@ -29,6 +29,7 @@ struct FwdParams {
     const int32_t* block_table;
     int block_size, max_blocks;
     int kv_rows;             // rows one gather may address: L (contiguous) or the pool size
+    int kv_fp8;              // 1: kv holds 656-byte fp8 rows (k_rope unused), narrow variants only
     int nsplit;              // KV splits per (token, head group)
     int ntiles;              // ceil(TOPK / tile_rows)
     int hgroups;             // H / heads_per_group

@@ -30,6 +30,7 @@
 // so that every exponential is one v_exp_f32; max/sum leave the kernel in
 // natural units.
 #include <hip/hip_runtime.h>
+#include <type_traits>
 #include <float.h>
 #include <stdint.h>
 
@@ -663,15 +664,162 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd_wide(FwdParams p) 
     }
 }
 
+// ============================================================ fp8 kv rows
+// FP8 KV cache row (656 bytes per token, the layout of DeepSeek-V3.2's FP8
+// MLA cache): 512 OCP float8 e4m3 latent values, 4 fp32 scales (scale i
+// covers dims 128 i .. 128 i + 127), then the 64 bf16 rope values.  A tile's
+// rows land as stored (656-byte stride) in one of two raw LDS stages; every
+// wave then expands a quarter of the latent dims of all its rows,
+//   kv[d] = bf16(fp32(e4m3[d]) * scale[d / 128])      (both roundings RNE),
+// into one bf16 tile laid out and swizzled like Ring's kv region, so the MFMA
+// code reads it unchanged.  Rope values are read from the raw rows.
+constexpr int kFp8Row = 656;
+constexpr int kFp8ScaleOff = 512;
+constexpr int kFp8RopeOff = 528;
+
+template <int BN_>
+struct RingFp8 {
+    static constexpr int BN = BN_;
+    static constexpr int NSTAGE = 2;
+    static constexpr int RAW_BYTES = BN * kFp8Row;       // one raw stage
+    static constexpr int KV_OFF = NSTAGE * RAW_BYTES;     // bf16 latent tile [BN][1024]
+    static constexpr int IDX_OFF = KV_OFF + BN * 1024;
+    static constexpr int FLAG_OFF = IDX_OFF + DSA_IDX_CAP * 4;
+    static constexpr int LDS_BYTES = FLAG_OFF + 16;
+    static constexpr int KV_PER_WAVE = BN / kWaves;  // one load per row, rope included
+    static constexpr int LOADS_PER_TILE = KV_PER_WAVE;
+    static_assert(LDS_BYTES <= 160 * 1024, "LDS budget");
+    static_assert(RAW_BYTES % 16 == 0, "16-byte aligned stages");
+    __device__ static uint32_t raw(uint32_t lds, int t) { return lds + (uint32_t)(t % NSTAGE) * RAW_BYTES; }
+};
+
+// The kv cache (or pool) as bytes, from the first row of the addressed range.
+__device__ __forceinline__ const char* fp8_base(const FwdParams& p, int b) {
+    const int64_t rows = p.block_table ? 0 : (int64_t)b * p.L;
+    return reinterpret_cast<const char*>(p.kv) + rows * kFp8Row;
+}
+
+// One fp8 row through a descriptor at its 64-bit address with a 656-byte
+// range; lanes 0..40 each load 16 bytes to m0 + 16 * lane (the other lanes
+// are masked off, so nothing lands past the row).
+__device__ __forceinline__ rsrc_t fp8_row_rsrc(const char* base, uint32_t row) {
+    const uint64_t a = reinterpret_cast<uint64_t>(base) + (uint64_t)row * kFp8Row;
+    rsrc_t r;
+    r[0] = (int)(uint32_t)a;
+    r[1] = (int)((a >> 32) & 0xffff);
+    r[2] = kFp8Row;
+    r[3] = 0x00020000;
+    return r;
+}
+
+template <class R>
+__device__ __forceinline__ void issue_tile_fp8(const FwdParams& p, const char* base, int t, uint32_t raw_stage,
+                                               uint32_t idx_lds, int wave, int lane) {
+    const int rows = p.kv_rows;
+    const int r0 = wave * R::KV_PER_WAVE;
+    const int my_id = lds_load<int>(idx_lds + 4 * (t * R::BN + r0 + (lane % R::KV_PER_WAVE)));
+    const uint32_t my_row = (uint32_t)min(max(my_id, 0), rows - 1);
+    const uint32_t voff = (uint32_t)lane << 4;
+#pragma unroll
+    for (int rr = 0; rr < R::KV_PER_WAVE; ++rr) {
+        const rsrc_t rs = fp8_row_rsrc(base, __builtin_amdgcn_readlane(my_row, rr));
+        if (lane < kFp8Row / 16) gather_lanes(raw_stage + (r0 + rr) * kFp8Row, rs, voff);
+    }
+}
+
+// One lane's 128 latent values (16-byte chunks 16 b .. 16 b + 15 of its row,
+// raw bytes at src, scale sc) into the swizzled bf16 row at dst.
+__device__ __forceinline__ void expand_block(uint32_t src, float sc, uint32_t dst, uint32_t sw, uint32_t b) {
+    i32x4 v[8];
+#pragma unroll
+    for (int m = 0; m < 8; ++m) v[m] = lds_load<i32x4>(src + 16 * m);
+    // A power-of-two scale 2^k (k in [-100, 100]) makes fp32(e4m3) * scale
+    // exact in fp32 and in bf16, and v_cvt_scalef32_pk_bf16_fp8 -- which
+    // applies only the exponent of its scale -- then yields the same bits in
+    // one instruction per two values.  The branch is uniform per wave.
+    const uint32_t sb = __float_as_uint(sc);
+    const uint32_t sexp = (sb >> 23) & 0xffu;
+    const bool pow2 = (sb & 0x807fffffu) == 0 && sexp >= 27u && sexp <= 227u;
+    auto store = [&](int m, int h, const bf16x8& o) {
+        const uint32_t chunk = 16u * b + (uint32_t)(2 * m + h);  // logical: dims 8 chunk ..
+        lds_store<bf16x8>(dst + ((chunk ^ sw) << 4), o);
+    };
+    if (__all(pow2)) {
+#pragma unroll
+        for (int m = 0; m < 8; ++m) {
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                bf16x8 o;
+#pragma unroll
+                for (int d = 0; d < 2; ++d) {
+                    const int w = v[m][2 * h + d];
+                    const auto lo = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, sc, false);
+                    const auto hi = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, sc, true);
+                    o[4 * d + 0] = lo[0];
+                    o[4 * d + 1] = lo[1];
+                    o[4 * d + 2] = hi[0];
+                    o[4 * d + 3] = hi[1];
+                }
+                store(m, h, o);
+            }
+        }
+    } else {
+#pragma unroll
+        for (int m = 0; m < 8; ++m) {
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {  // 8 values = one 16-byte bf16 chunk
+                bf16x8 o;
+#pragma unroll
+                for (int d = 0; d < 2; ++d) {
+                    const int w = v[m][2 * h + d];
+                    const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8(w, false);
+                    const auto hi = __builtin_amdgcn_cvt_pk_f32_fp8(w, true);
+                    o[4 * d + 0] = (__bf16)(lo[0] * sc);
+                    o[4 * d + 1] = (__bf16)(lo[1] * sc);
+                    o[4 * d + 2] = (__bf16)(hi[0] * sc);
+                    o[4 * d + 3] = (__bf16)(hi[1] * sc);
+                }
+                store(m, h, o);
+            }
+        }
+    }
+}
+
+// Tile-wide expansion (head slices share rows): wave w expands dims
+// 128 w .. 128 w + 127 of every row; lane l takes row l.  Reads at a 656-byte
+// stride hit 16 distinct bank groups per pass, and so do the swizzled writes.
+template <class R>
+__device__ __forceinline__ void dequant_tile(uint32_t raw_stage, uint32_t kv_tile, int wave, int lane) {
+    static_assert(R::BN == 64, "one row per lane");
+    const uint32_t row = (uint32_t)lane;
+    expand_block(raw_stage + row * kFp8Row + 128u * (uint32_t)wave,
+                 lds_load<float>(raw_stage + row * kFp8Row + kFp8ScaleOff + 4u * (uint32_t)wave),
+                 kv_tile + row * 1024u, (uint32_t)sw_kv(lane), (uint32_t)wave);
+}
+
+// Per-wave expansion of the 16 rows a wave alone reads (one head slice): lane
+// l takes row rowbase + l % 16 and block 2 ((l / 16) % 2) + l / 32.  A pass
+// serves lanes 16 l / 16 .. (k-groups 0 and 1, or 2 and 3), i.e. blocks 0 and
+// 2 (or 1 and 3), 256 bytes apart -- the same bank groups -- over
+// complementary sets of 8 rows, which the 656-byte row stride (9 r mod 16 in
+// 16-byte groups) spreads over all 16 bank groups.
+__device__ __forceinline__ void dequant_rows(uint32_t raw_stage, uint32_t kv_tile, int rowbase, int lane) {
+    const uint32_t row = (uint32_t)(rowbase + (lane & 15));
+    const uint32_t b = 2u * (uint32_t)((lane >> 4) & 1) + (uint32_t)(lane >> 5);
+    expand_block(raw_stage + row * kFp8Row + 128u * b,
+                 lds_load<float>(raw_stage + row * kFp8Row + kFp8ScaleOff + 4u * b),
+                 kv_tile + row * 1024u, (uint32_t)sw_kv((int)row), b);
+}
+
 // ==================================================================== narrow
 // HW head-waves of 16 heads x KW kv-waves (HW * KW == 4).
 //
 // 16x16x32 operand layouts (lane i, g = i >> 4, n = i & 15):
 //   A[m = n][k = 8g + j], B[k = 8g + j][n = n], C[m = 4g + r][n = n].
-template <int HW, int KW>
+template <int HW, int KW, bool FP8 = false>
 __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd_narrow(FwdParams p) {
     static_assert(HW * KW == kWaves, "narrow variant shape");
-    using R = Ring<64, 2>;
+    using R = std::conditional_t<FP8, RingFp8<64>, Ring<64, 2>>;
     constexpr int kBN = R::BN;
     constexpr int RPW = kBN / KW;   // tile rows per wave
     constexpr int NSUB = RPW / 16;  // 16-row subtiles per wave
@@ -717,6 +865,11 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd_narrow(FwdParams p
     store_indices(ids, idx_lds);
     lds_barrier();
     const Gather gt = make_gather(p, c.b);
+    const char* fp8_rows = fp8_base(p, c.b);
+    auto issue = [&](int t) {
+        if constexpr (FP8) issue_tile_fp8<R>(p, fp8_rows, t, R::raw(lds, t), idx_lds, wave, lane);
+        else issue_tile<R>(p, gt, t, R::stage(lds, t), idx_lds, wave, lane);
+    };
 
     // ---- per-lane LDS offsets (see the wide variant).
     const int rowbase = kw * RPW;
@@ -750,15 +903,30 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd_narrow(FwdParams p
     l_run = 0.f;
     if (pass == 1) m_ref = m_true;
     bool overflow = false;
-    if (c.nt > 0) issue_tile<R>(p, gt, 0, R::stage(lds, 0), idx_lds, wave, lane);
+    if (c.nt > 0) issue(0);
     wait_vmcnt<0>();  // Q and tile 0 (see the wide variant)
 
     for (int t = 0; t < c.nt; ++t) {
-        R::wait_tile(t, c.nt);
+        wait_vmcnt<0>();  // this wave's gathers of tile t (two stages: nothing else in flight)
         lds_barrier();
-        if (t + 1 < c.nt) issue_tile<R>(p, gt, t + 1, R::stage(lds, t + 1), idx_lds, wave, lane);
+        if (t + 1 < c.nt) issue(t + 1);
 
-        const uint32_t stage = R::stage(lds, t);
+        uint32_t stage, rope_rows;  // latent tile (bf16, swizzled); raw fp8 rows (rope)
+        if constexpr (FP8) {
+            if constexpr (HW == 1) {
+                // one head slice: a wave alone reads its rows, so it expands
+                // them itself and needs no barrier (LDS is in order per wave)
+                dequant_rows(R::raw(lds, t), lds + R::KV_OFF, rowbase, lane);
+            } else {
+                dequant_tile<R>(R::raw(lds, t), lds + R::KV_OFF, wave, lane);
+                lds_barrier();  // the expanded tile is complete
+            }
+            stage = lds + R::KV_OFF;
+            rope_rows = R::raw(lds, t);
+        } else {
+            stage = R::stage(lds, t);
+            rope_rows = 0;
+        }
         // ---- S^T = K . Q^T for this wave's rows.  Steps run k-step major over
         // the NSUB subtiles in an explicit 4-deep LDS pipeline (the scheduler is
         // fenced per step); with one subtile the k-steps alternate between two
@@ -777,8 +945,11 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd_narrow(FwdParams p
         auto kfrag = [&](int step) -> bf16x8 {
             const int ks = step / NSUB, s = step % NSUB;
             const int row = rowbase + 16 * s + n16;
-            return ks < 16 ? lds_load<bf16x8>(stage + row * 1024 + qk_g + ((uint32_t)(16 * ks) ^ qk_x))
-                           : lds_load<bf16x8>(stage + R::KV_BYTES + row * 128 + rp_off[ks - 16]);
+            if (ks < 16) return lds_load<bf16x8>(stage + row * 1024 + qk_g + ((uint32_t)(16 * ks) ^ qk_x));
+            if constexpr (FP8)
+                return lds_load<bf16x8>(rope_rows + row * kFp8Row + kFp8RopeOff + ((4 * (ks - 16) + g) << 4));
+            else
+                return lds_load<bf16x8>(stage + R::KV_BYTES + row * 128 + rp_off[ks - 16]);
         };
         {
             bf16x8 kf[4];
@@ -1011,9 +1182,15 @@ int64_t fwd_grid(const FwdParams& p) { return (int64_t)p.rowgroups * p.hgroups; 
 
 int launch_fwd(const FwdParams& p, int hpg, int kvw, int bn, int stages, int mfma, hipStream_t stream) {
     if (!fwd_variant_exists(hpg, kvw, bn, stages, mfma)) return (int)hipErrorInvalidValue;
+    if (p.kv_fp8 && mfma != 16) return (int)hipErrorInvalidValue;  // fp8 rows: narrow variants only
     if (mfma == 32) {
         if (hpg == 128) return launch(sparse_mla_fwd_wide<4, 1, 32, 4>, p, stream);
         return launch(sparse_mla_fwd_wide<2, 2, 64, 2>, p, stream);
+    }
+    if (p.kv_fp8) {
+        if (hpg == 64) return launch(sparse_mla_fwd_narrow<4, 1, true>, p, stream);
+        if (hpg == 32) return launch(sparse_mla_fwd_narrow<2, 2, true>, p, stream);
+        return launch(sparse_mla_fwd_narrow<1, 4, true>, p, stream);
     }
     if (hpg == 64) return launch(sparse_mla_fwd_narrow<4, 1>, p, stream);
     if (hpg == 32) return launch(sparse_mla_fwd_narrow<2, 2>, p, stream);

@@ -147,20 +147,34 @@ int dsa_fwd_main(const uint16_t* q, const uint16_t* kv, const uint16_t* q_rope,
  *                 num_blocks * block_size must be below 33554432.  Indices stay
  *                 logical and are masked as in dsa_fwd; a slot whose block
  *                 entry lies outside [0, num_blocks) is masked as well.
+ *   kv_format   : DSA_KV_BF16 (0): kv and k_rope as above.  DSA_KV_FP8 (1): kv
+ *                 holds 656-byte rows, [B, L, 656] bytes (or a [num_blocks,
+ *                 block_size, 656] pool) -- 512 OCP float8 e4m3 latent values,
+ *                 4 fp32 scales (scale i covers dims 128 i .. 128 i + 127), 64
+ *                 bf16 rope values -- and k_rope is unused (may be NULL).  The
+ *                 kernel computes with kv[d] = bf16(fp32(e4m3[d]) * scale[d /
+ *                 128]) (both roundings to nearest even) and the rope values;
+ *                 only narrow plans (mfma 16) read fp8 rows.
+ *   reserved32, reserved : must be zero.
  */
+#define DSA_KV_BF16 0
+#define DSA_KV_FP8 1
 typedef struct dsa_fwd_options {
     float scale;
     int32_t block_size;
     int32_t max_blocks;
     int32_t num_blocks;
     const int32_t* block_table;
-    int64_t reserved[2];
+    int32_t kv_format;
+    int32_t reserved32;
+    int64_t reserved[1];
 } dsa_fwd_options;
 
 /*
  * dsa_fwd and dsa_fwd_main with options (opts NULL = all defaults).  No
- * reference counterpart: the softmax scale and paged kv are the next steps
- * beyond the reference's fixed-scale, contiguous-cache operator.
+ * reference counterpart: the softmax scale, paged kv and the fp8 kv row
+ * format are the next steps beyond the reference's fixed-scale,
+ * contiguous bf16 cache operator (dsa/api.py:30-33).
  */
 int dsa_fwd_opts(const uint16_t* q, const uint16_t* kv, const uint16_t* q_rope,
                  const uint16_t* k_rope, const int32_t* idx,
@@ -168,6 +182,14 @@ int dsa_fwd_opts(const uint16_t* q, const uint16_t* kv, const uint16_t* q_rope,
                  float* part_o, float* part_m, float* part_l,
                  int B, int SQ, int H, int L, int TOPK,
                  const dsa_fwd_options* opts, const dsa_plan* plan, hipStream_t stream);
+
+/*
+ * dsa_plan_for for a call with options: with kv_format DSA_KV_FP8 it plans
+ * among the variants that read fp8 rows (no reference counterpart; see
+ * dsa_fwd_options).  Pure host logic.
+ */
+int dsa_plan_for_opts(int B, int SQ, int H, int L, int TOPK, int num_cus, const dsa_fwd_options* opts,
+                      dsa_plan* out);
 
 int dsa_fwd_main_opts(const uint16_t* q, const uint16_t* kv, const uint16_t* q_rope,
                       const uint16_t* k_rope, const int32_t* idx,

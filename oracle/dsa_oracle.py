@@ -25,6 +25,12 @@ Functions and the reference code each one restates:
                          reference takes contiguous kv only), so paged runs are
                          checked against the same ``reference``.
 
+* ``e4m3_decode`` / ``dequant_fp8_rows`` -- the fp8 kv cache rows (656
+                         bytes: 512 OCP e4m3, 4 fp32 scales, 64 bf16 rope; no
+                         reference counterpart, which takes bf16 kv only,
+                         dsa/api.py:30-33) back to the bf16 kv and rope the
+                         kernels compute with, so fp8 runs are checked against
+                         the same ``reference``.
 * ``indexer_logits_ref`` / ``indexer_topk_ref`` / ``float_key`` -- the
                          lightning indexer (no reference counterpart: the
                          reference takes the indices as an input,
@@ -43,6 +49,10 @@ scaled_dot_product_attention (which also pins ``scale``), FP64 brute force,
 closed forms of the uniform family, index-permutation / -1-removal /
 duplicate-counting invariants, an identity block table and a gather
 restatement for ``unpage``, and planted mistakes that each check must reject.
+FP8 rows: ``e4m3_decode`` against torch's float8_e4m3fn on all 256 codes and
+against hand-worked values; ``dequant_fp8_rows`` against an element-wise
+restatement, with planted mistakes (a 64-dim scale block, rounding to bf16
+before the scale) rejected.
 Indexer: FP64 brute-force logits (planted: ReLU or head weights dropped),
 brute-force selection over tie-heavy rows, -0.0 / +0.0, -inf and short rows
 (planted: ties taken from the top), and the float-key order.
@@ -129,6 +139,34 @@ def mask_unbacked(indices, ok):
     backed = torch.gather(ok[:, None, None, :].expand(-1, indices.shape[1], 1, -1), 3, rows)
     indices[inside & ~backed] = -1
     return indices
+
+
+def e4m3_decode(codes):
+    """OCP float8 e4m3 (bias 7, no infinities, S.1111.111 = NaN) to float32,
+    from the format's definition: normal (1 + m/8) 2^(e-7), subnormal
+    (m/8) 2^-6."""
+    c = np.asarray(codes, dtype=np.uint8).astype(np.int64)
+    sign = np.where(c & 0x80, -1.0, 1.0)
+    e = (c >> 3) & 15
+    m = c & 7
+    mag = np.where(e == 0, m / 8.0 * 2.0 ** -6, (1.0 + m / 8.0) * 2.0 ** (e - 7))
+    out = (sign * mag).astype(np.float32)
+    out[(c & 0x7F) == 0x7F] = np.nan
+    return out
+
+
+def dequant_fp8_rows(rows):
+    """FP8 kv cache rows ``[..., 656]`` (uint8) -> ``(kv [..., 512], rope
+    [..., 64])`` bf16: ``kv[d] = bf16(fp32(e4m3[d]) * scale[d // 128])`` with
+    fp32 round-to-nearest-even product and bf16 round-to-nearest-even (no
+    reference counterpart; the DeepSeek-V3.2 FP8 MLA cache row layout)."""
+    u8 = rows.cpu().contiguous()
+    lead = u8.shape[:-1]
+    vals = torch.from_numpy(e4m3_decode(u8[..., :512].numpy())).reshape(*lead, 4, 128)
+    scales = u8[..., 512:528].contiguous().view(torch.float32).reshape(*lead, 4, 1)
+    kv = (vals * scales).reshape(*lead, 512).bfloat16()
+    rope = u8[..., 528:656].contiguous().view(torch.bfloat16)
+    return kv, rope
 
 
 def indexer_logits_ref(q_idx, k_idx, weights, lengths, chunk: int = 64):

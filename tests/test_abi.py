@@ -22,7 +22,7 @@ def declared_functions():
 def test_header_declares_the_expected_entry_points():
     assert declared_functions() == sorted(
         ["dsa_version", "dsa_last_error", "dsa_plan_for", "dsa_plan_check", "dsa_partial_elems",
-         "dsa_fwd", "dsa_fwd_main", "dsa_fwd_opts", "dsa_fwd_main_opts", "dsa_merge",
+         "dsa_fwd", "dsa_fwd_main", "dsa_fwd_opts", "dsa_fwd_main_opts", "dsa_plan_for_opts", "dsa_merge",
          "dsa_indexer_logits", "dsa_indexer_topk"])
 
 
@@ -41,9 +41,14 @@ def test_version_and_last_error():
 
 def test_struct_layout_matches_header():
     assert ctypes.sizeof(_lib.DsaPlan) == 32
-    # float, 3 x int32, pointer, 2 x int64
+    # float, 3 x int32, pointer, 2 x int32, int64
     assert ctypes.sizeof(_lib.DsaFwdOptions) == 40
     assert _lib.DsaFwdOptions.block_table.offset == 16
+    assert _lib.DsaFwdOptions.kv_format.offset == 24
+    assert _lib.DsaFwdOptions.reserved.offset == 32
+    text = HEADER.read_text()
+    assert "#define DSA_KV_BF16 0" in text and "#define DSA_KV_FP8 1" in text
+    assert (_lib.KV_BF16, _lib.KV_FP8) == (0, 1)
 
 
 def test_plan_for_rejects_bad_shapes():
@@ -115,6 +120,40 @@ def test_fwd_opts_validate_before_any_launch():
     # misaligned block table
     o = _lib.DsaFwdOptions(block_size=64, max_blocks=16, num_blocks=100, block_table=ctypes.c_void_p((1 << 20) + 2))
     assert _opts_call(lib, o, L=1024) < 0 and b"aligned" in lib.dsa_last_error()
+
+
+def test_fp8_kv_format_validation():
+    lib = _lib.load()
+    assert _opts_call(lib, _lib.DsaFwdOptions(kv_format=2)) < 0 and b"kv_format" in lib.dsa_last_error()
+    assert _opts_call(lib, _lib.DsaFwdOptions(reserved32=1)) < 0 and b"reserved" in lib.dsa_last_error()
+    # fp8 rows are read by the narrow (mfma 16) variants only; k_rope may be NULL
+    fake = ctypes.c_void_p(1 << 20)
+    wide = _lib.DsaPlan(128, 32, 1, 1, 4, 32)
+    o = _lib.DsaFwdOptions(kv_format=_lib.KV_FP8)
+    rc = lib.dsa_fwd_opts(fake, fake, fake, None, fake, fake, fake, fake, None, None, None,
+                          1, 1, 128, 1024, 64, ctypes.byref(o), ctypes.byref(wide), None)
+    assert rc < 0 and b"narrow" in lib.dsa_last_error()
+    # without fp8 a NULL k_rope is an error
+    narrow = _lib.DsaPlan(64, 64, 1, 1, 2, 16)
+    rc = lib.dsa_fwd_opts(fake, fake, fake, None, fake, fake, fake, fake, None, None, None,
+                          1, 1, 128, 1024, 64, ctypes.byref(_lib.DsaFwdOptions()), ctypes.byref(narrow), None)
+    assert rc < 0 and b"NULL" in lib.dsa_last_error()
+
+
+@pytest.mark.parametrize("shape", [(8, 1, 128, 32768, 2048), (64, 2, 16, 65536, 2048), (1, 4096, 128, 32768, 2048)])
+def test_fp8_planner_keeps_to_narrow_variants(shape):
+    lib = _lib.load()
+    plan = _lib.DsaPlan()
+    o = _lib.DsaFwdOptions(kv_format=_lib.KV_FP8)
+    assert lib.dsa_plan_for_opts(*shape, 256, ctypes.byref(o), ctypes.byref(plan)) == 0
+    assert plan.mfma == 16 and lib.dsa_plan_check(ctypes.byref(plan), *shape) == 0
+    bad = _lib.DsaFwdOptions(kv_format=5)
+    assert lib.dsa_plan_for_opts(*shape, 256, ctypes.byref(bad), ctypes.byref(plan)) < 0
+    # NULL options plan like dsa_plan_for
+    ref = _lib.DsaPlan()
+    assert lib.dsa_plan_for(*shape, 256, ctypes.byref(ref)) == 0
+    assert lib.dsa_plan_for_opts(*shape, 256, None, ctypes.byref(plan)) == 0
+    assert bytes(plan) == bytes(ref)
 
 
 def test_indexer_entry_points_validate_before_any_launch():

@@ -218,3 +218,58 @@ def test_indexer_topk_rejections():
         dsa_amd.indexer_topk(logits.double(), lengths, 10)
     with pytest.raises(ValueError):  # CPU tensors: the selection runs on a ROCm GPU only
         dsa_amd.indexer_topk(logits, lengths, 10)
+
+
+# ------------------------------------------------------------ fp8 kv rows
+def test_fp8_rows_shape_contract():
+    q = torch.zeros(2, 3, 16, 512, dtype=torch.bfloat16)
+    qr = torch.zeros(2, 3, 16, 64, dtype=torch.bfloat16)
+    ids = torch.zeros(2, 3, 1, 64, dtype=torch.int32)
+    rows = torch.zeros(2, 100, 1, 656, dtype=torch.uint8)
+    kr = torch.zeros(2, 100, 1, 64, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="k_rope must be None"):
+        _check_inputs(q, rows, qr, kr, ids)
+    with pytest.raises(ValueError, match="k_rope is required"):
+        _check_inputs(q, torch.zeros(2, 100, 1, 512, dtype=torch.bfloat16), qr, None, ids)
+    with pytest.raises(ValueError, match="656"):
+        _check_inputs(q, torch.zeros(3, 100, 1, 656, dtype=torch.uint8), qr, None, ids)
+    # shapes pass; the CPU device is then rejected like any other input
+    with pytest.raises(ValueError, match="ROCm GPU"):
+        _check_inputs(q, rows, qr, None, ids)
+
+
+def test_fp8_plans_are_narrow():
+    for shape in ((8, 1, 128, 32768, 2048), (1, 4096, 128, 32768, 2048)):
+        config, _, _ = plan_call(shape, None, 256, kv_fp8=True)
+        assert config.mfma == 16
+    with pytest.raises(ValueError, match="narrow"):
+        plan_call((1, 1, 128, 8192, 2048), Tuning(128, 32, 1, stages=4), 256, kv_fp8=True)
+
+
+def test_quantize_kv_fp8_rows():
+    g = torch.Generator().manual_seed(5)
+    kv = (torch.randn(2, 7, 1, 512, generator=g) * 3).bfloat16()
+    kv[0, 0, 0, 128:256] = 0  # an all-zero block keeps scale 1
+    kr = torch.randn(2, 7, 1, 64, generator=g).bfloat16()
+    rows = dsa_amd.quantize_kv_fp8(kv, kr, pow2_scales=False)
+    assert rows.shape == (2, 7, 1, 656) and rows.dtype == torch.uint8
+    scales = rows[..., 512:528].contiguous().view(torch.float32)
+    amax = kv.float().reshape(2, 7, 1, 4, 128).abs().amax(-1)
+    expect = torch.where(amax > 0, amax / 448.0, torch.ones_like(amax))
+    assert torch.equal(scales, expect)
+    # default: the smallest power of two with amax / scale <= 448
+    p2 = dsa_amd.quantize_kv_fp8(kv, kr)[..., 512:528].contiguous().view(torch.float32)
+    m, _ = torch.frexp(p2)
+    assert (m == 0.5).all()
+    assert (amax / p2 <= 448.0).all() and ((amax == 0) | (amax / p2 > 224.0)).all()
+    assert torch.equal(rows[..., 528:].contiguous().view(torch.bfloat16), kr)
+    codes = rows[..., :512].contiguous().view(torch.float8_e4m3fn).float().reshape(2, 7, 1, 4, 128)
+    assert codes.abs().max() <= 448.0
+    back = (codes * scales[..., None]).reshape(2, 7, 1, 512)
+    # e4m3 keeps 3 mantissa bits: each value within 2^-4 of its block maximum's scale step
+    err = (back - kv.float()).abs().reshape(2, 7, 1, 4, 128).amax(-1)
+    assert (err <= amax / 16 + 1e-30).all()
+    with pytest.raises(ValueError):
+        dsa_amd.quantize_kv_fp8(kv.float(), kr)
+    with pytest.raises(ValueError):
+        dsa_amd.quantize_kv_fp8(kv, kr[..., :32])

@@ -397,3 +397,54 @@ def test_indexer_topk_planted_tie_order_is_caught():
     got = O.indexer_topk_ref(logits, lengths, 3)
     assert got[0, 0, 0].tolist() == [0, 1, 2]  # ties keep the lowest s
     assert got[0, 0, 0].tolist() != [7, 8, 9]
+
+
+# ------------------------------------------------------------ fp8 kv rows
+def test_e4m3_decode_matches_definition_and_torch():
+    codes = np.arange(256, dtype=np.uint8)
+    got = O.e4m3_decode(codes)
+    ref = torch.from_numpy(codes).view(torch.float8_e4m3fn).float().numpy()
+    assert np.array_equal(got, ref, equal_nan=True)
+    # hand-worked: 0x38 = 1.0, 0x7E = 448 (max), 0x01 = 2^-9 (smallest subnormal), 0xC0 = -2.0
+    assert got[0x38] == 1.0 and got[0x7E] == 448.0 and got[0x01] == 2.0 ** -9 and got[0xC0] == -2.0
+    assert np.isnan(got[0x7F]) and np.isnan(got[0xFF]) and np.isinf(got).sum() == 0
+
+
+def _fp8_rows(seed, lead=(2, 5, 1)):
+    g = torch.Generator().manual_seed(seed)
+    codes = torch.randint(0, 256, (*lead, 512), generator=g, dtype=torch.uint8)
+    codes[(codes & 0x7F) == 0x7F] = 0x38  # no NaN codes
+    scales = torch.rand((*lead, 4), generator=g) * 0.5 + 1e-3
+    rope = torch.randn((*lead, 64), generator=g).bfloat16()
+    rows = torch.cat([codes, scales.view(torch.uint8), rope.view(torch.uint8)], -1)
+    return rows, codes, scales, rope
+
+
+def test_dequant_fp8_rows_elementwise():
+    rows, codes, scales, rope = _fp8_rows(31)
+    kv, rp = O.dequant_fp8_rows(rows)
+    assert torch.equal(rp, rope)
+    vals = O.e4m3_decode(codes.numpy())
+    flat_kv = kv.float().reshape(-1, 512).numpy()
+    flat_vals = vals.reshape(-1, 512)
+    flat_sc = scales.reshape(-1, 4).numpy()
+    for r in (0, 3, 9):
+        for d in (0, 127, 128, 300, 511):
+            prod = np.float32(flat_vals[r, d]) * np.float32(flat_sc[r, d // 128])
+            expect = torch.tensor(float(prod), dtype=torch.float32).bfloat16().float().item()
+            assert flat_kv[r, d] == expect
+
+
+def test_dequant_fp8_planted_mistakes_are_caught():
+    rows, codes, scales, rope = _fp8_rows(32)
+    kv, rp = O.dequant_fp8_rows(rows)
+    vals = torch.from_numpy(O.e4m3_decode(codes.numpy())).reshape(*codes.shape[:-1], 4, 128)
+    # each 128-dim block scaled by its neighbour's scale (an off-by-one block index)
+    shifted = (vals * scales.roll(1, -1)[..., None]).reshape(kv.shape).bfloat16()
+    # the scale rounded to bf16 before the product
+    coarse = (vals * scales.bfloat16().float()[..., None]).reshape(kv.shape).bfloat16()
+    # rope bytes read as the 64 values before them
+    assert not torch.equal(shifted, kv)
+    assert not torch.equal(coarse, kv)
+    wrong_rope = rows[..., 464:592].contiguous().view(torch.bfloat16)
+    assert not torch.equal(wrong_rope, rp)
