@@ -92,6 +92,14 @@ class Call:
         self.config = config
         self.plan = config.to_c()
         dev = q.device
+        # Fused-merge plan: one launch per call, the main kernel merging in
+        # its last workgroup per (token, head group) on these arrival counters.
+        self.fused = config.fused_merge and config.split > 1
+        if self.fused:
+            self.counters = torch.zeros(b * sq * (h // config.bm), device=dev, dtype=torch.int32)
+            if self.opts is None:
+                self.opts = _lib.DsaFwdOptions()
+            self.opts.arrivals = self.counters.data_ptr()
         self.out = torch.empty_like(q)
         self.mx = torch.empty((b, 1, sq, h), device=dev, dtype=torch.float32)
         self.sm = torch.empty_like(self.mx)
@@ -107,7 +115,10 @@ class Call:
 
     def main(self, stream):
         b, sq, h, length, k = self.shape
-        if self.opts is None:
+        if self.fused:
+            rc = self.lib.dsa_fwd_opts(*self.args, b, sq, h, length, k, ctypes.byref(self.opts),
+                                       ctypes.byref(self.plan), stream)
+        elif self.opts is None:
             rc = self.lib.dsa_fwd_main(*self.args, b, sq, h, length, k, ctypes.byref(self.plan), stream)
         else:
             rc = self.lib.dsa_fwd_main_opts(*self.args, b, sq, h, length, k, ctypes.byref(self.opts),
@@ -116,7 +127,7 @@ class Call:
             _lib.check(rc, "dsa_fwd_main")
 
     def merge(self, stream):
-        if self.po is None:
+        if self.po is None or self.fused:
             return
         b, sq, h, _, _ = self.shape
         rc = self.lib.dsa_merge(self.args[8], self.args[9], self.args[10], self.args[5], self.args[6],
@@ -259,7 +270,8 @@ def run(name, args):
         v = [int(x) for x in args.plan.split(",")]
         bm, split, kv_waves, mfma = v[:4]
         bn, stages = (v[4], v[5]) if len(v) > 4 else (64, 2)
-        config = Tuning(bm, bn, split, kv_waves=kv_waves, stages=stages, mfma=mfma)
+        fused = bool(v[6]) if len(v) > 6 else False
+        config = Tuning(bm, bn, split, kv_waves=kv_waves, stages=stages, mfma=mfma, fused_merge=fused)
     print(f"[bench] {name} shape={shape} plan={config} rotate={rotate}", file=sys.stderr, flush=True)
     sets = [baseline_inputs(name, seed=args.seed + i, device="cuda", cpu_recipe=False) for i in range(rotate)]
     if args.fp8:  # the same inputs with kv and k_rope written as 656-byte fp8 rows
@@ -468,7 +480,7 @@ def main():
     ap.add_argument("--config", default="c2_decode_b8", choices=sorted(BASELINE_CONFIGS))
     ap.add_argument("--all", action="store_true", help="one line per configuration C2..C5")
     ap.add_argument("--rotate", type=int, default=0, help="input sets to cycle (default per workload)")
-    ap.add_argument("--plan", default="", help="override the plan: bm,split,kv_waves,mfma[,bn,stages]")
+    ap.add_argument("--plan", default="", help="override the plan: bm,split,kv_waves,mfma[,bn,stages[,fused]]")
     ap.add_argument("--seed", type=int, default=20261102)
     ap.add_argument("--paged", type=int, default=0, metavar="BLOCK",
                     help="run the workload on paged kv (block pools of BLOCK rows, random block table)")

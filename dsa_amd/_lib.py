@@ -26,7 +26,8 @@ class DsaPlan(ctypes.Structure):
         ("kv_waves", ctypes.c_int32),
         ("stages", ctypes.c_int32),
         ("mfma", ctypes.c_int32),
-        ("reserved", ctypes.c_int32 * 2),
+        ("fused_merge", ctypes.c_int32),
+        ("reserved", ctypes.c_int32),
     ]
 
 
@@ -41,7 +42,7 @@ class DsaFwdOptions(ctypes.Structure):
         ("block_table", ctypes.c_void_p),
         ("kv_format", ctypes.c_int32),
         ("reserved32", ctypes.c_int32),
-        ("reserved", ctypes.c_int64 * 1),
+        ("arrivals", ctypes.c_void_p),
     ]
 
 

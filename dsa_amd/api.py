@@ -4,12 +4,14 @@ Mirrors the reference's public operator ``dsa.forward`` (dsa/api.py:76-132):
 same positional arguments, tensor contract, return triple and exception types,
 with the device requirement moved from Ascend ("npu") to a ROCm GPU.  The work
 is one main-kernel launch plus, when the plan splits the KV range, one FP32
-merge launch, both enqueued through the C ABI on the current stream.  There
-is no CPU or fallback path.
+merge -- a second launch, or, with a fused-merge plan, the main kernel's last
+workgroup per (token, head group) -- enqueued through the C ABI on the
+current stream.  There is no CPU or fallback path.
 """
 from __future__ import annotations
 
 import ctypes
+import threading
 from dataclasses import dataclass
 
 import torch
@@ -128,8 +130,29 @@ def plan_call(shape, config=None, cores: int = 256, kv_fp8: bool = False):
     partials = None
     if config.split > 1:
         partials = ((batch, queries, config.split, heads, HEAD_DIM), (batch, queries, config.split, heads))
-        launches.append(Launch("merge_partials", tokens * ((heads + 1) // 2), 256, 0))
+        if not config.fused_merge:
+            launches.append(Launch("merge_partials", tokens * ((heads + 1) // 2), 256, 0))
     return config, partials, tuple(launches)
+
+
+# Arrival counters of the in-kernel merge, one zeroed int32 array per (device,
+# stream).  Every call leaves its counters at zero once its kernel completes,
+# so calls in stream order share one array; a call on another stream gets its
+# own.  The arrays hold no inputs or results: only the counters' zeros persist.
+_arrivals_lock = threading.Lock()
+_arrivals = {}
+
+
+def _arrival_counters(device, stream: int, count: int) -> torch.Tensor:
+    key = (device.index, stream)
+    with _arrivals_lock:
+        buf = _arrivals.get(key)
+        if buf is None or buf.numel() < count:
+            # zero-filled on this stream, so ordered before the kernel that uses it
+            size = max(count, 2 * buf.numel() if buf is not None else 1024)
+            buf = torch.zeros(size, device=device, dtype=torch.int32)
+            _arrivals[key] = buf
+        return buf
 
 
 def forward(q, kv, q_rope, k_rope, indices, *, config=None, cores=None, return_kernels=False,
@@ -183,8 +206,9 @@ def forward(q, kv, q_rope, k_rope, indices, *, config=None, cores=None, return_k
     args = (ptr(q), ptr(kv), ptr(q_rope), ptr(k_rope), ptr(indices),
             ptr(output), ptr(maximum), ptr(denominator), ptr(part_o), ptr(part_m), ptr(part_l),
             batch, queries, heads, length, topk)
+    fused = config.fused_merge and config.split > 1
     with torch.cuda.device(device):
-        if scale is None and block_table is None and not fp8:
+        if scale is None and block_table is None and not fp8 and not fused:
             rc = _lib.load().dsa_fwd(*args, ctypes.byref(plan), ctypes.c_void_p(stream))
         else:
             opts = _lib.DsaFwdOptions()
@@ -195,6 +219,9 @@ def forward(q, kv, q_rope, k_rope, indices, *, config=None, cores=None, return_k
                 opts.max_blocks = block_table.shape[1]
                 opts.num_blocks = kv.shape[0]
                 opts.block_table = block_table.data_ptr()
+            if fused:
+                counters = _arrival_counters(device, stream, batch * queries * (heads // config.bm))
+                opts.arrivals = counters.data_ptr()
             rc = _lib.load().dsa_fwd_opts(*args, ctypes.byref(opts), ctypes.byref(plan), ctypes.c_void_p(stream))
     _lib.check(rc, "dsa_fwd")
     result = (output, maximum, denominator)

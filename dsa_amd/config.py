@@ -12,7 +12,10 @@ Ascend Cube/Vector pipeline; here the plan describes gfx950 workgroups:
 * ``stages``   -- LDS ring depth (2 or 4);
 * ``mfma``     -- heads per wave: 32 (v_mfma_f32_32x32x16_bf16: bm 128 with
                   bn 32 and 4 stages, or bm 64 with kv_waves 2) or 16
-                  (v_mfma_f32_16x16x32_bf16: bm 64, 32 or 16, bn 64, 2 stages).
+                  (v_mfma_f32_16x16x32_bf16: bm 64, 32 or 16, bn 64, 2 stages);
+* ``fused_merge`` -- with split in [2, 16] on a narrow plan (mfma 16), the
+                  main kernel's last workgroup per (token, head group) merges
+                  the partials: one launch instead of two, the same bits.
 
 Unlike the reference, shapes outside the table are accepted: the library's
 planner (``dsa_plan_for``) derives a plan for any supported shape.
@@ -35,16 +38,19 @@ class Tuning:
     kv_waves: int = 1
     stages: int = 2
     mfma: int = 32
+    fused_merge: bool = False
 
     def to_c(self) -> _lib.DsaPlan:
         p = _lib.DsaPlan()
         p.heads_per_group, p.tile_rows, p.split = self.bm, self.bn, self.split
         p.kv_waves, p.stages, p.mfma = self.kv_waves, self.stages, self.mfma
+        p.fused_merge = 1 if self.fused_merge else 0
         return p
 
     @staticmethod
     def from_c(p: _lib.DsaPlan) -> "Tuning":
-        return Tuning(p.heads_per_group, p.tile_rows, p.split, p.kv_waves, p.stages, p.mfma)
+        return Tuning(p.heads_per_group, p.tile_rows, p.split, p.kv_waves, p.stages, p.mfma,
+                      bool(p.fused_merge))
 
 
 # (batch, query length, heads, KV length, number of selected indices).
@@ -99,6 +105,8 @@ def check_tuning(config: Tuning, shape) -> None:
     if any(type(v) is not int
            for v in (config.bm, config.bn, config.split, config.kv_waves, config.stages, config.mfma)):
         raise ValueError("Tuning fields must be int")
+    if type(config.fused_merge) is not bool:
+        raise ValueError("Tuning.fused_merge must be a bool")
     b, sq, h, length, topk = shape
     plan = config.to_c()
     _lib.check(_lib.load().dsa_plan_check(ctypes.byref(plan), b, sq, h, length, topk), "invalid Tuning")
@@ -108,6 +116,9 @@ def check_tuning(config: Tuning, shape) -> None:
 # table (dsa/config.py:42-59): the library planner's choice (dsa_plan_for, a
 # cost model fitted to MI355X measurements), except where a measured sweep
 # found a faster plan (decode_b32, prefill_q16, prefill_q64, decode_b4_h128).
+# The in-kernel merge pays where a (token, head group) has little to merge
+# (2 splits x 16 heads: C3 69.3 -> 65.3 µs); with 512 KiB groups (C1, C2)
+# one CU reading them back costs more than the merge kernel.
 SELECTED = {
     "decode_b1": Tuning(16, 64, 16, kv_waves=4, mfma=16),
     "decode_b8": Tuning(32, 64, 8, kv_waves=2, mfma=16),
@@ -115,7 +126,7 @@ SELECTED = {
     "decode_tp8": Tuning(16, 64, 16, kv_waves=4, mfma=16),
     "prefill_q16": Tuning(32, 64, 4, kv_waves=2, mfma=16),
     "prefill_q64": Tuning(32, 64, 1, kv_waves=2, mfma=16),
-    "prefill_tp8": Tuning(16, 64, 2, kv_waves=4, mfma=16),
+    "prefill_tp8": Tuning(16, 64, 2, kv_waves=4, mfma=16, fused_merge=True),
     "prefill_k512": Tuning(32, 64, 1, kv_waves=2, mfma=16),
     "decode_b4_h128": Tuning(16, 64, 8, kv_waves=4, mfma=16),
     "prefill_b4_h128": Tuning(128, 32, 1, stages=4),
@@ -127,7 +138,7 @@ SELECTED = {
     "prefill_b4_h16": Tuning(16, 64, 1, kv_waves=4, mfma=16),
     "c1_decode_b1": Tuning(16, 64, 16, kv_waves=4, mfma=16),
     "c2_decode_b8": Tuning(32, 64, 8, kv_waves=2, mfma=16),
-    "c3_decode_h16_mtp": Tuning(16, 64, 2, kv_waves=4, mfma=16),
+    "c3_decode_h16_mtp": Tuning(16, 64, 2, kv_waves=4, mfma=16, fused_merge=True),
     "c4_prefill_h16": Tuning(16, 64, 1, kv_waves=4, mfma=16),
     "c5_prefill_h128": Tuning(128, 32, 1, stages=4),
 }

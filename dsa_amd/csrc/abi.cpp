@@ -34,6 +34,10 @@ int hip_fail(int err, const char* what) {
 
 int ceil_div(int a, int b) { return (a + b - 1) / b; }
 
+// Largest split the in-kernel merge handles (its per-head weights are held in
+// registers, one per split).
+constexpr int kMaxFusedSplit = 16;
+
 int check_shape(int B, int SQ, int H, int L, int TOPK) {
     if (B <= 0 || SQ <= 0 || H <= 0 || L <= 0 || TOPK <= 0)
         return fail(-1, "all of B, SQ, H, L, TOPK must be positive (got %d, %d, %d, %d, %d)", B, SQ, H, L, TOPK);
@@ -71,6 +75,12 @@ int dsa_plan_check(const dsa_plan* plan, int B, int SQ, int H, int L, int TOPK) 
         return fail(-1, "split must be in [1, %d] for TOPK=%d (got %d)", ntiles, TOPK, split);
     if (ceil_div(ntiles, split) * bn > DSA_IDX_CAP)
         return fail(-1, "split %d leaves more than %d slots per workgroup (TOPK=%d)", split, DSA_IDX_CAP, TOPK);
+    if (plan->fused_merge != 0 && plan->fused_merge != 1)
+        return fail(-1, "fused_merge must be 0 or 1 (got %d)", plan->fused_merge);
+    if (plan->fused_merge && (mfma != 16 || split > kMaxFusedSplit))
+        return fail(-1, "fused_merge needs a narrow plan (mfma 16) with split <= %d (got mfma=%d split=%d)",
+                    kMaxFusedSplit, mfma, split);
+    if (plan->reserved) return fail(-1, "plan reserved field must be zero");
     g_err[0] = 0;
     return 0;
 }
@@ -81,8 +91,9 @@ namespace {
 
 // The planner behind dsa_plan_for; `fp8` restricts it to the variants that
 // read 656-byte fp8 kv rows (the narrow ones) and prices their gathers and
-// per-tile expansion.
-int plan_impl(int B, int SQ, int H, int L, int TOPK, int num_cus, bool fp8, dsa_plan* out) {
+// per-tile expansion; `fuse` lets it price the in-kernel merge for narrow
+// plans with split <= kMaxFusedSplit.
+int plan_impl(int B, int SQ, int H, int L, int TOPK, int num_cus, bool fp8, bool fuse, dsa_plan* out) {
     if (!out) return fail(-1, "out is NULL");
     if (int rc = check_shape(B, SQ, H, L, TOPK)) return rc;
     if (num_cus <= 0) return fail(-1, "num_cus must be positive (got %d)", num_cus);
@@ -93,7 +104,10 @@ int plan_impl(int B, int SQ, int H, int L, int TOPK, int num_cus, bool fp8, dsa_
     // first gather), a cost per tile, and an epilogue (row-wave merge and
     // partial stores); the gathered rows are also bounded by the HBM rate the
     // active CUs reach; a split adds the merge kernel, bounded by its
-    // parallelism.
+    // parallelism, or -- merged in the kernel -- a tail in which the last
+    // workgroup of each group reads the group's partials back on one CU
+    // (measured ≈30 GB/s: C3's 64 KiB groups cost ≈0.4 µs over the main
+    // kernel, C1's and C2's 512 KiB groups 17-18 µs).
     struct Variant {
         int hpg, kvw, bn, stages, mfma;
         double tile_cycles, epilogue_cycles;
@@ -109,6 +123,7 @@ int plan_impl(int B, int SQ, int H, int L, int TOPK, int num_cus, bool fp8, dsa_
     constexpr double kHbmBytesPerUs = 4.8e6, kCuBytesPerUs = 3.0e4;                // sustained gather rates
     constexpr double kMergeUs = 2.0, kMergeWgBytesPerUs = 4.2e4, kMergeBytesPerUs = 6.0e6;
     constexpr double kFp8TileCycles = 1200.0;  // expanding a 64-row fp8 tile to bf16 in LDS
+    constexpr double kFusedUs = 0.5, kFusedBytesPerUs = 3.0e4;  // in-kernel merge: count-in, one CU's read rate
     const int64_t tokens = (int64_t)B * SQ;
     const double gathered = (double)tokens * TOPK * (fp8 ? 656.0 : 1152.0);
     double best = -1.0;
@@ -138,11 +153,17 @@ int plan_impl(int B, int SQ, int H, int L, int TOPK, int num_cus, bool fp8, dsa_
                                                                                     : kMergeBytesPerUs;
                 merge_us = kMergeUs + bytes / bw;
             }
-            const double cost = kLaunchUs + main_us + merge_us;
+            double cost = kLaunchUs + main_us + merge_us;
+            int fused = 0;
+            if (fuse && split > 1 && split <= kMaxFusedSplit && v.mfma == 16) {
+                const double group_bytes = (double)split * v.hpg * 2056.0;
+                const double fused_cost = kLaunchUs + main_us + kFusedUs + group_bytes / kFusedBytesPerUs;
+                if (fused_cost < cost) cost = fused_cost, fused = 1;
+            }
             if (best < 0.0 || cost < best * 0.999) {
                 best = cost;
                 p.heads_per_group = v.hpg, p.kv_waves = v.kvw, p.tile_rows = v.bn, p.stages = v.stages;
-                p.mfma = v.mfma, p.split = split;
+                p.mfma = v.mfma, p.split = split, p.fused_merge = fused;
             }
         }
     }
@@ -156,14 +177,14 @@ int plan_impl(int B, int SQ, int H, int L, int TOPK, int num_cus, bool fp8, dsa_
 extern "C" {
 
 int dsa_plan_for(int B, int SQ, int H, int L, int TOPK, int num_cus, dsa_plan* out) {
-    return plan_impl(B, SQ, H, L, TOPK, num_cus, false, out);
+    return plan_impl(B, SQ, H, L, TOPK, num_cus, false, true, out);
 }
 
 int dsa_plan_for_opts(int B, int SQ, int H, int L, int TOPK, int num_cus, const dsa_fwd_options* opts,
                       dsa_plan* out) {
     if (opts && opts->kv_format != DSA_KV_BF16 && opts->kv_format != DSA_KV_FP8)
         return fail(-1, "kv_format must be DSA_KV_BF16 (0) or DSA_KV_FP8 (1) (got %d)", opts->kv_format);
-    return plan_impl(B, SQ, H, L, TOPK, num_cus, opts && opts->kv_format == DSA_KV_FP8, out);
+    return plan_impl(B, SQ, H, L, TOPK, num_cus, opts && opts->kv_format == DSA_KV_FP8, true, out);
 }
 
 int dsa_partial_elems(const dsa_plan* plan, int B, int SQ, int H, int64_t* part_o_elems,
@@ -209,7 +230,8 @@ int fwd_impl(const uint16_t* q, const uint16_t* kv, const uint16_t* q_rope, cons
     if (opts) {
         if (opts->kv_format != DSA_KV_BF16 && opts->kv_format != DSA_KV_FP8)
             return fail(-1, "kv_format must be DSA_KV_BF16 (0) or DSA_KV_FP8 (1) (got %d)", opts->kv_format);
-        if (opts->reserved32 || opts->reserved[0]) return fail(-1, "reserved option fields must be zero");
+        if (opts->reserved32) return fail(-1, "reserved option fields must be zero");
+        if ((uintptr_t)opts->arrivals & 3) return fail(-1, "arrivals must be 4-byte aligned");
         if (opts->scale != 0.0f) {
             if (!(opts->scale > 0.0f) || !std::isfinite(opts->scale))
                 return fail(-1, "scale must be a positive finite number (got %g)", (double)opts->scale);
@@ -238,13 +260,16 @@ int fwd_impl(const uint16_t* q, const uint16_t* kv, const uint16_t* q_rope, cons
         int err = (int)hipGetDevice(&dev);
         if (!err) err = (int)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
         if (err) return hip_fail(err, "querying the CU count");
-        if (int rc = plan_impl(B, SQ, H, L, TOPK, cus, fp8, &local)) return rc;
+        if (int rc = plan_impl(B, SQ, H, L, TOPK, cus, fp8, opts && opts->arrivals, &local)) return rc;
         plan = &local;
     } else if (int rc = dsa_plan_check(plan, B, SQ, H, L, TOPK)) {
         return rc;
     }
     if (fp8 && plan->mfma != 16) return fail(-1, "fp8 kv rows need a narrow plan (mfma 16)");
     const bool split = plan->split > 1;
+    // The in-kernel merge needs the caller's arrival counters; without them
+    // the merge kernel runs (same bits).
+    const bool fused = split && with_merge && plan->fused_merge && opts && opts->arrivals;
     if ((!split || with_merge) && (!out || !out_max || !out_sum)) return fail(-1, "NULL output pointer");
     if (split && (!part_o || !part_m || !part_l))
         return fail(-1, "split=%d needs part_o, part_m and part_l", plan->split);
@@ -283,11 +308,12 @@ int fwd_impl(const uint16_t* q, const uint16_t* kv, const uint16_t* q_rope, cons
     p.ntiles = ceil_div(TOPK, plan->tile_rows);
     p.hgroups = H / plan->heads_per_group;
     p.rowgroups = (int)rowgroups;
+    p.arrivals = fused ? opts->arrivals : nullptr;
 
     int rc = dsa::launch_fwd(p, plan->heads_per_group, plan->kv_waves, plan->tile_rows, plan->stages, plan->mfma,
                              stream);
     if (rc) return hip_fail(rc, "main kernel launch");
-    if (split && with_merge) {
+    if (split && with_merge && !fused) {
         rc = dsa::launch_merge(part_o, part_m, part_l, out, out_max, out_sum, B * SQ, H, plan->split, stream);
         if (rc) return hip_fail(rc, "merge launch");
     }

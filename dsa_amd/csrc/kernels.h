@@ -30,6 +30,11 @@ struct FwdParams {
     int block_size, max_blocks;
     int kv_rows;             // rows one gather may address: L (contiguous) or the pool size
     int kv_fp8;              // 1: kv holds 656-byte fp8 rows (k_rope unused), narrow variants only
+    // Non-NULL (nsplit in [2, 16], narrow variants): one arrival counter per
+    // (token, head group), zero on entry; the workgroup that arrives last
+    // merges the group's partials into out/out_max/out_sum and zeroes its
+    // counter again.  NULL: the partials are left for the merge kernel.
+    uint32_t* arrivals;
     int nsplit;              // KV splits per (token, head group)
     int ntiles;              // ceil(TOPK / tile_rows)
     int hgroups;             // H / heads_per_group

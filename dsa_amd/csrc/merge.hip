@@ -4,20 +4,19 @@
 //   out = bf16(sum_s w_s * u_s / l);  out_max = m;  out_sum = l.
 // One workgroup merges two heads of one token; each thread owns 4 of the 512
 // columns and streams the split partials with 16-byte loads, kBatch splits in
-// flight at a time.
+// flight at a time.  The arithmetic is merge_math.h's, which the main
+// kernel's in-kernel merge shares.
 #include <hip/hip_runtime.h>
 #include <float.h>
 #include <stdint.h>
 
 #include "kernels.h"
+#include "merge_math.h"
 
 namespace dsa {
 namespace {
 
-typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;
-typedef __attribute__((__vector_size__(4 * sizeof(__bf16)))) __bf16 bf16x4;
-
-constexpr float kLog2e = 1.4426950408889634f;
+typedef merge_f32x4 f32x4;
 
 constexpr int kBatch = 16;  // split partials loaded per batch (kept in flight together)
 
@@ -55,25 +54,17 @@ __global__ __launch_bounds__(256) void merge_kernel(const float* __restrict__ pa
 #pragma unroll
         for (int j = 0; j < kBatch; ++j) mb = fmaxf(mb, ms[j]);
         if (s0 > 0) {
-            const float alpha = __builtin_amdgcn_exp2f((m - mb) * kLog2e);
+            const float alpha = merge_weight(m, mb);
             l *= alpha;
             acc *= alpha;
         }
         m = mb;
 #pragma unroll
-        for (int j = 0; j < kBatch; ++j) {
-            const float w = __builtin_amdgcn_exp2f((ms[j] - m) * kLog2e);
-            l += w * ls[j];
-            acc += w * u[j];
-        }
+        for (int j = 0; j < kBatch; ++j)
+            if (s0 + j < nsplit) merge_add(merge_weight(ms[j], m), ls[j], u[j], l, acc);
     }
-    bf16x4 o;
-    o[0] = (__bf16)(acc[0] / l);
-    o[1] = (__bf16)(acc[1] / l);
-    o[2] = (__bf16)(acc[2] / l);
-    o[3] = (__bf16)(acc[3] / l);
     const int64_t orow = (int64_t)token * H + h;
-    *reinterpret_cast<bf16x4*>(out + orow * 512 + col) = o;
+    *reinterpret_cast<merge_bf16x4*>(out + orow * 512 + col) = merge_finish(acc, l);
     if ((threadIdx.x & 127) == 0) {
         out_max[orow] = m;
         out_sum[orow] = l;

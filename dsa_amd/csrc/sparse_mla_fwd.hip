@@ -35,6 +35,7 @@
 #include <stdint.h>
 
 #include "kernels.h"
+#include "merge_math.h"
 #include "../../include/dsa_mi355x.h"
 
 namespace dsa {
@@ -816,6 +817,111 @@ __device__ __forceinline__ void dequant_rows(uint32_t raw_stage, uint32_t kv_til
 //
 // 16x16x32 operand layouts (lane i, g = i >> 4, n = i & 15):
 //   A[m = n][k = 8g + j], B[k = 8g + j][n = n], C[m = 4g + r][n = n].
+// ---------------------------------------------------- in-kernel split merge
+// With p.arrivals set, every workgroup of a (token, head group) stores its
+// split partials with agent-coherent accesses (the cache policy of an
+// agent-scope atomic: sc1, written through to the level every XCD reads),
+// waits for them to complete, and counts itself in on the group's arrival
+// counter with an agent-scope atomic; the workgroup that arrives last reads
+// all the group's partials back with agent-coherent loads, merges them with
+// merge_math.h -- the merge kernel's arithmetic, so the bits are the same --
+// writes out, out_max and out_sum, and zeroes the counter for the next call.
+// Because every access to the partials is coherent at agent scope, no L2
+// writeback or invalidation (an agent-scope fence) is needed.  No workgroup
+// waits for another, so nothing depends on which workgroups are resident.
+//
+// A lane owns head `head` = head0 + hl and columns 16 cb + 4 g .. +3 for cb
+// in [cb_lo, cb_lo + NCB); its partials of split s live in the group's
+// head block of that split: part_o row (token * nsplit + s) * H + head0,
+// byte 2048 hl + 16 g + 64 cb.
+constexpr int kAgentCoherent = 16;  // buffer cache policy: sc1
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t group_block(const FwdParams& p, int token, int split, int head0,
+                                                              int heads) {
+    return __builtin_amdgcn_make_buffer_rsrc(p.part_o + (((int64_t)token * p.nsplit + split) * p.H + head0) * 512,
+                                             (short)0, heads * 2048, 0x00020000);
+}
+
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+
+template <int NCB>
+__device__ __forceinline__ void merge_if_last(const FwdParams& p, const WgCoords& c, int head0, int heads, int hl,
+                                              int g, bool writes_ml, int cb_lo, uint32_t flag_lds) {
+    static_assert(NCB % 8 == 0, "column blocks per lane");
+    wait_vmcnt<0>();  // this wave's partial stores have completed ...
+    lds_barrier();    // ... and every other wave's
+    const int64_t group = (int64_t)c.token * p.hgroups + c.hgi;
+    if (threadIdx.x == 0) {
+        const uint32_t before =
+            __hip_atomic_fetch_add(p.arrivals + group, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        lds_store<int>(flag_lds, before + 1 == (uint32_t)p.nsplit ? 1 : 0);
+    }
+    lds_barrier();
+    if (__builtin_amdgcn_readfirstlane(lds_load<int>(flag_lds)) == 0) return;
+    if (threadIdx.x == 0) __hip_atomic_store(p.arrivals + group, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+
+    const int S = p.nsplit;  // 2..16, checked on the host
+    const int head = head0 + hl;
+    const int64_t row0 = (int64_t)c.token * S * p.H + head;  // (m, l) of split s: row0 + s * H
+    float ms[16], ls[16];
+#pragma unroll
+    for (int s = 0; s < 16; ++s) {
+        ms[s] = s < S ? __hip_atomic_load(p.part_m + row0 + (int64_t)s * p.H, __ATOMIC_RELAXED,
+                                          __HIP_MEMORY_SCOPE_AGENT)
+                      : -FLT_MAX;
+        ls[s] = s < S ? __hip_atomic_load(p.part_l + row0 + (int64_t)s * p.H, __ATOMIC_RELAXED,
+                                          __HIP_MEMORY_SCOPE_AGENT)
+                      : 0.f;
+    }
+    float m = -FLT_MAX;
+#pragma unroll
+    for (int s = 0; s < 16; ++s) m = fmaxf(m, ms[s]);
+    float w[16];
+    float l = 0.f;
+#pragma unroll
+    for (int s = 0; s < 16; ++s) {
+        w[s] = merge_weight(ms[s], m);
+        if (s < S) l = __builtin_fmaf(w[s], ls[s], l);
+    }
+    const uint32_t voff = (uint32_t)(hl * 2048 + 16 * g + 64 * cb_lo);
+    uint16_t* orow = p.out + ((int64_t)c.token * p.H + head) * 512 + 4 * g + 16 * cb_lo;
+#pragma unroll
+    for (int c8 = 0; c8 < NCB; c8 += 8) {
+        merge_f32x4 acc[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[i] = merge_f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s0 = 0; s0 < 16; s0 += 4) {
+            if (s0 < S) {
+                merge_f32x4 u[4][8];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    if (s0 + j < S) {
+                        const __amdgpu_buffer_rsrc_t rs = group_block(p, c.token, s0 + j, head0, heads);
+#pragma unroll
+                        for (int i = 0; i < 8; ++i)
+                            u[j][i] = __builtin_bit_cast(
+                                merge_f32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, voff + 64 * (c8 + i), 0,
+                                                                                   kAgentCoherent));
+                    }
+                }
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    if (s0 + j < S)
+#pragma unroll
+                        for (int i = 0; i < 8; ++i) merge_add_cols(w[s0 + j], u[j][i], acc[i]);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            *reinterpret_cast<merge_bf16x4*>(orow + 16 * (c8 + i)) = merge_finish(acc[i], l);
+    }
+    if (writes_ml) {
+        p.out_max[(int64_t)c.token * p.H + head] = m;
+        p.out_sum[(int64_t)c.token * p.H + head] = l;
+    }
+}
+
 template <int HW, int KW, bool FP8 = false>
 __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd_narrow(FwdParams p) {
     static_assert(HW * KW == kWaves, "narrow variant shape");
@@ -1149,7 +1255,7 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd_narrow(FwdParams p
             p.out_max[(int64_t)c.token * p.H + head] = m_nat;
             p.out_sum[(int64_t)c.token * p.H + head] = l_fin;
         }
-    } else {
+    } else if (p.arrivals == nullptr) {
         const int64_t prow = ((int64_t)c.token * p.nsplit + c.sp) * p.H + head;
         float* orow = p.part_o + prow * 512 + 4 * g;
 #pragma unroll
@@ -1159,6 +1265,23 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd_narrow(FwdParams p
             p.part_m[prow] = m_nat;
             p.part_l[prow] = l_fin;
         }
+    } else {
+        // In-kernel merge: the same partials, stored agent-coherent.
+        constexpr int kHeads = 16 * HW;
+        const int head0 = c.hgi * kHeads, hl = hw * 16 + n16;
+        const __amdgpu_buffer_rsrc_t rs = group_block(p, c.token, c.sp, head0, kHeads);
+        const uint32_t voff = (uint32_t)(hl * 2048 + 16 * g);
+#pragma unroll
+        for (int cb = 0; cb < 32; ++cb)
+            if (cb >= cb_lo && cb < cb_hi)
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, oacc[cb] * to_true), rs,
+                                                       voff + 64 * cb, 0, kAgentCoherent);
+        if (g == 0 && kw == 0) {
+            const int64_t prow = ((int64_t)c.token * p.nsplit + c.sp) * p.H + head;
+            __hip_atomic_store(p.part_m + prow, m_nat, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(p.part_l + prow, l_fin, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        merge_if_last<32 / KW>(p, c, head0, kHeads, hl, g, g == 0 && kw == 0, cb_lo, flag_lds);
     }
 }
 

@@ -58,6 +58,14 @@ extern "C" {
  *                     heads_per_group 128 with tile_rows 32 and 4 stages, or 64
  *                     with kv_waves 2) or 16 (v_mfma_f32_16x16x32_bf16;
  *                     heads_per_group 64, 32 or 16; tile_rows 64, 2 stages)
+ *   fused_merge     : 0 or 1.  1 (mfma 16 and split <= 16 only): the merge
+ *                     runs inside the main kernel -- the last workgroup of
+ *                     each (token, head group) to finish merges its partials,
+ *                     one launch instead of two -- whenever the call supplies
+ *                     dsa_fwd_options.arrivals; otherwise (dsa_fwd, or no
+ *                     arrivals) the merge kernel runs.  Same bits either way.
+ *                     No effect when split == 1.
+ *   reserved        : must be zero.
  */
 typedef struct dsa_plan {
     int32_t heads_per_group;
@@ -66,7 +74,8 @@ typedef struct dsa_plan {
     int32_t kv_waves;
     int32_t stages;
     int32_t mfma;
-    int32_t reserved[2];
+    int32_t fused_merge;
+    int32_t reserved;
 } dsa_plan;
 
 /* Library version, (major << 16) | minor. */
@@ -155,7 +164,15 @@ int dsa_fwd_main(const uint16_t* q, const uint16_t* kv, const uint16_t* q_rope,
  *                 kernel computes with kv[d] = bf16(fp32(e4m3[d]) * scale[d /
  *                 128]) (both roundings to nearest even) and the rope values;
  *                 only narrow plans (mfma 16) read fp8 rows.
- *   reserved32, reserved : must be zero.
+ *   arrivals    : NULL, or uint32 [B * SQ * (H / heads_per_group)] arrival
+ *                 counters for a plan with fused_merge = 1 and split > 1 (one
+ *                 per (token, head group)).  They must be zero before the
+ *                 first call; every call leaves them zero again once its
+ *                 kernel has completed, so one array serves any number of
+ *                 calls in stream order.  Calls that can run at the same time
+ *                 (other streams) need arrays of their own.  Ignored by
+ *                 dsa_fwd_main_opts and by plans that do not fuse the merge.
+ *   reserved32  : must be zero.
  */
 #define DSA_KV_BF16 0
 #define DSA_KV_FP8 1
@@ -167,14 +184,16 @@ typedef struct dsa_fwd_options {
     const int32_t* block_table;
     int32_t kv_format;
     int32_t reserved32;
-    int64_t reserved[1];
+    uint32_t* arrivals;
 } dsa_fwd_options;
 
 /*
  * dsa_fwd and dsa_fwd_main with options (opts NULL = all defaults).  No
  * reference counterpart: the softmax scale, paged kv and the fp8 kv row
  * format are the next steps beyond the reference's fixed-scale,
- * contiguous bf16 cache operator (dsa/api.py:30-33).
+ * contiguous bf16 cache operator (dsa/api.py:30-33); the arrival counters
+ * fold the reference's second launch (the merge task, dsa/api.py:124-128)
+ * into the main kernel.
  */
 int dsa_fwd_opts(const uint16_t* q, const uint16_t* kv, const uint16_t* q_rope,
                  const uint16_t* k_rope, const int32_t* idx,

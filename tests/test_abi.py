@@ -41,11 +41,12 @@ def test_version_and_last_error():
 
 def test_struct_layout_matches_header():
     assert ctypes.sizeof(_lib.DsaPlan) == 32
-    # float, 3 x int32, pointer, 2 x int32, int64
+    assert _lib.DsaPlan.fused_merge.offset == 24 and _lib.DsaPlan.reserved.offset == 28
+    # float, 3 x int32, pointer, 2 x int32, pointer
     assert ctypes.sizeof(_lib.DsaFwdOptions) == 40
     assert _lib.DsaFwdOptions.block_table.offset == 16
     assert _lib.DsaFwdOptions.kv_format.offset == 24
-    assert _lib.DsaFwdOptions.reserved.offset == 32
+    assert _lib.DsaFwdOptions.arrivals.offset == 32
     text = HEADER.read_text()
     assert "#define DSA_KV_BF16 0" in text and "#define DSA_KV_FP8 1" in text
     assert (_lib.KV_BF16, _lib.KV_FP8) == (0, 1)
@@ -120,6 +121,35 @@ def test_fwd_opts_validate_before_any_launch():
     # misaligned block table
     o = _lib.DsaFwdOptions(block_size=64, max_blocks=16, num_blocks=100, block_table=ctypes.c_void_p((1 << 20) + 2))
     assert _opts_call(lib, o, L=1024) < 0 and b"aligned" in lib.dsa_last_error()
+
+
+def test_fused_merge_plan_checks():
+    lib = _lib.load()
+    shape = (8, 1, 128, 32768, 2048)
+    ok = _lib.DsaPlan(32, 64, 8, 2, 2, 16, 1)
+    assert lib.dsa_plan_check(ctypes.byref(ok), *shape) == 0
+    # split 1 is accepted (nothing to merge)
+    assert lib.dsa_plan_check(ctypes.byref(_lib.DsaPlan(32, 64, 1, 2, 2, 16, 1)), *shape) == 0
+    for bad, msg in ((_lib.DsaPlan(32, 64, 8, 2, 2, 16, 2), b"0 or 1"),
+                     (_lib.DsaPlan(64, 64, 4, 2, 2, 32, 1), b"narrow"),      # wide variant
+                     (_lib.DsaPlan(32, 64, 17, 2, 2, 16, 1), b"split <= 16"),
+                     (_lib.DsaPlan(32, 64, 8, 2, 2, 16, 0, 1), b"reserved")):
+        assert lib.dsa_plan_check(ctypes.byref(bad), *shape) < 0
+        assert msg in lib.dsa_last_error(), lib.dsa_last_error()
+    # misaligned arrival counters are rejected before any launch
+    o = _lib.DsaFwdOptions(arrivals=ctypes.c_void_p((1 << 20) + 2))
+    assert _opts_call(lib, o) < 0 and b"arrivals" in lib.dsa_last_error()
+
+
+@pytest.mark.parametrize("shape", [(8, 1, 128, 32768, 2048), (64, 2, 16, 65536, 2048), (1, 1, 128, 8192, 2048),
+                                   (1, 4096, 128, 32768, 2048)])
+def test_planner_fused_merge_only_where_supported(shape):
+    lib = _lib.load()
+    plan = _lib.DsaPlan()
+    assert lib.dsa_plan_for(*shape, 256, ctypes.byref(plan)) == 0
+    if plan.fused_merge:
+        assert plan.mfma == 16 and 1 < plan.split <= 16
+    assert lib.dsa_plan_check(ctypes.byref(plan), *shape) == 0
 
 
 def test_fp8_kv_format_validation():

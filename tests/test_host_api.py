@@ -102,6 +102,20 @@ def test_plan_call_allocations_and_launches():
     assert config.split == 1 and partials is None and len(launches) == 1
 
 
+def test_plan_call_fused_merge_is_one_launch():
+    shape = CASE_SHAPES["c3_decode_h16_mtp"]
+    config, partials, launches = plan_call(shape, cores=256)
+    assert config.fused_merge and config.split == 2
+    # partials are still written (and read back by the last workgroup); no merge launch
+    assert partials == ((64, 2, 2, 16, 512), (64, 2, 2, 16))
+    assert len(launches) == 1 and launches[0].name.startswith("sparse_mla_fwd_narrow")
+    # a fused plan goes through the same library check as any other
+    with pytest.raises(ValueError, match="fused_merge"):
+        plan_call(CASE_SHAPES["c2_decode_b8"], Tuning(64, 64, 2, kv_waves=2, mfma=32, fused_merge=True))
+    with pytest.raises(ValueError, match="bool"):
+        plan_call(shape, Tuning(16, 64, 2, kv_waves=4, mfma=16, fused_merge=1))
+
+
 def test_plan_call_explicit_tuning_and_errors():
     shape = (1, 1, 128, 8192, 2048)
     config, partials, _ = plan_call(shape, Tuning(32, 64, 4, kv_waves=2, mfma=16))
