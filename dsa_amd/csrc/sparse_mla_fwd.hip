@@ -1009,13 +1009,27 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd_narrow(FwdParams p
     l_run = 0.f;
     if (pass == 1) m_ref = m_true;
     bool overflow = false;
+    // One head slice (HW == 1) on bf16 rows: every wave gathers exactly the
+    // rows it computes on (rows 16 w .. 16 w + 15 of each tile), so its
+    // pipeline needs no workgroup barrier and keeps two tiles in flight,
+    // issuing tile t + 2 into the stage it has just finished reading.
+    constexpr bool kOwnRows = HW == 1 && !FP8;
     if (c.nt > 0) issue(0);
     wait_vmcnt<0>();  // Q and tile 0 (see the wide variant)
+    if constexpr (kOwnRows)
+        if (c.nt > 1) issue(1);
 
     for (int t = 0; t < c.nt; ++t) {
-        wait_vmcnt<0>();  // this wave's gathers of tile t (two stages: nothing else in flight)
-        lds_barrier();
-        if (t + 1 < c.nt) issue(t + 1);
+        if constexpr (kOwnRows) {
+            if (t > 0) {  // tile t has landed; tile t + 1 may stay in flight
+                if (t + 1 < c.nt) wait_vmcnt<R::LOADS_PER_TILE>();
+                else wait_vmcnt<0>();
+            }
+        } else {
+            wait_vmcnt<0>();  // this wave's gathers of tile t (two stages: nothing else in flight)
+            lds_barrier();
+            if (t + 1 < c.nt) issue(t + 1);
+        }
 
         uint32_t stage, rope_rows;  // latent tile (bf16, swizzled); raw fp8 rows (rope)
         if constexpr (FP8) {
@@ -1166,6 +1180,11 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd_narrow(FwdParams p
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
+        if constexpr (kOwnRows)
+            if (t + 2 < c.nt) {
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this wave's reads of the stage are done
+                issue(t + 2);
+            }
     }
 
     // ---- workgroup vote: does any head need pass 1?
