@@ -369,6 +369,9 @@ class IndexerCall:
         self.largs = [p(q), p(k), p(w), p(lengths), p(self.logits)]
         self.targs = [p(self.logits), p(lengths), p(self.indices)]
         self.lib = _lib.load()
+        # few rows: the segmented selection (8 workgroups per row) over a workspace
+        self.ws_bytes = self.lib.dsa_indexer_topk_ws_bytes(q.shape[0], q.shape[1], k.shape[1], topk)
+        self.ws = torch.empty(max(self.ws_bytes, 1), device=q.device, dtype=torch.uint8)
 
     def main(self, stream):
         b, sq, hi, length, _ = self.shape
@@ -376,9 +379,13 @@ class IndexerCall:
         if rc:
             _lib.check(rc, "dsa_indexer_logits")
 
-    def merge(self, stream):  # the second launch of a call: the selection
+    def merge(self, stream):  # the second step of a call: the selection
         b, sq, _, length, topk = self.shape
-        rc = self.lib.dsa_indexer_topk(*self.targs, b, sq, length, topk, stream)
+        if self.ws_bytes > 0:
+            rc = self.lib.dsa_indexer_topk_ws(*self.targs, b, sq, length, topk, ctypes.c_void_p(self.ws.data_ptr()),
+                                              self.ws_bytes, stream)
+        else:
+            rc = self.lib.dsa_indexer_topk(*self.targs, b, sq, length, topk, stream)
         if rc:
             _lib.check(rc, "dsa_indexer_topk")
 

@@ -72,6 +72,8 @@ SIGNATURES = {
     "dsa_merge": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _vp]),
     "dsa_indexer_logits": (_i32, [_vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _vp]),
     "dsa_indexer_topk": (_i32, [_vp, _vp, _vp, _i32, _i32, _i32, _i32, _vp]),
+    "dsa_indexer_topk_ws_bytes": (_i64, [_i32, _i32, _i32, _i32]),
+    "dsa_indexer_topk_ws": (_i32, [_vp, _vp, _vp, _i32, _i32, _i32, _i32, _vp, _i64, _vp]),
 }
 
 _lock = threading.Lock()

@@ -416,4 +416,24 @@ int dsa_indexer_topk(const float* logits, const int32_t* lengths, int32_t* indic
     return 0;
 }
 
+int64_t dsa_indexer_topk_ws_bytes(int B, int SQ, int L, int TOPK) {
+    if (B <= 0 || SQ <= 0 || L <= 0 || TOPK <= 0 || L >= (1 << 28) || (int64_t)B * SQ >= (1 << 22)) return 0;
+    return dsa::indexer_topk_ws_bytes(B * SQ, L);
+}
+
+int dsa_indexer_topk_ws(const float* logits, const int32_t* lengths, int32_t* indices, int B, int SQ, int L,
+                        int TOPK, void* workspace, int64_t workspace_bytes, hipStream_t stream) {
+    const int64_t need = dsa_indexer_topk_ws_bytes(B, SQ, L, TOPK);
+    if (!workspace || need == 0) return dsa_indexer_topk(logits, lengths, indices, B, SQ, L, TOPK, stream);
+    if (!logits || !lengths || !indices) return fail(-1, "NULL pointer argument");
+    if (workspace_bytes < need)
+        return fail(-1, "workspace of %lld bytes is below the %lld needed", (long long)workspace_bytes,
+                    (long long)need);
+    if ((uintptr_t)workspace & 15) return fail(-1, "workspace must be 16-byte aligned");
+    const int rc = dsa::launch_indexer_topk_seg(logits, lengths, indices, workspace, B * SQ, L, TOPK, stream);
+    if (rc) return hip_fail(rc, "segmented indexer top-k launch");
+    g_err[0] = 0;
+    return 0;
+}
+
 }  // extern "C"

@@ -29,6 +29,7 @@
 // order.  A row of up to 65536 candidates is read from memory once, plus its
 // gathered entries.
 #include <hip/hip_runtime.h>
+#include <type_traits>
 #include <float.h>
 #include <stdint.h>
 
@@ -656,6 +657,411 @@ __global__ __launch_bounds__(kTopkThreads, 1) void indexer_topk_kernel(const flo
         topk_select<false>(sh, row, dst, n, K);
 }
 
+// ------------------------------------------------ segmented top-k (few rows)
+// With few rows, one 1024-thread workgroup per row leaves most CUs idle and is
+// bound by its own VALU issue.  The segmented path splits every row over
+// kSegWgs workgroups of 256 threads, each owning the contiguous segment
+// [p * seg, (p + 1) * seg) of s, in three launches (the kernel boundaries are
+// the only synchronisation; the workspace needs no initialisation):
+//   1. seg_hist: per segment, the histogram of the keys' bits 31..20;
+//   2. seg_cand: every workgroup finds, from its row's histograms, the bin
+//      bin0 holding the TOPK-th largest key; it records how many of its
+//      entries lie above bin0 and stores the keys of its entries in bin0
+//      (the candidates) in its own range of the row's candidate list;
+//   3. seg_emit: every workgroup resolves, from the candidates, the threshold
+//      key T and how many entries equal to T each segment takes (ties go to
+//      the lowest s, i.e. to the earliest segments), then writes its selected
+//      s in ascending order at its offset: key > T, or key == T among its
+//      first takes.
+// Same selection and order as topk_select.
+constexpr int kSegWgs = 8;          // workgroups per row
+constexpr int kSegThreads = 256;
+constexpr int kSegMaxRows = 32;     // rows * kSegWgs workgroups at most: 256
+constexpr int kSegCandCap = 8192;   // candidates resolved from LDS; more are read from the workspace
+constexpr int kSegKeys = 16;        // keys per thread in flight (4096 per workgroup and batch)
+
+// Workspace words of one row: histograms [kSegWgs][kBins0] of key bits
+// 31..20 and coarse ones [kSegWgs][kCoarse] of bits 31..26; per segment
+// [kSegWgs][4] (entries above bin0, candidate count, bin0, entries to take
+// from bin0); candidate keys [L], segment p's from p * seg on (a segment's
+// candidates keep its order); rounded to 4 words.
+constexpr int kCoarse = 64;
+__host__ __device__ inline int64_t seg_row_words(int L) {
+    return ((int64_t)kSegWgs * (kBins0 + kCoarse) + 4 * kSegWgs + (int64_t)L + 3) & ~(int64_t)3;
+}
+struct SegRow {
+    uint32_t* base;
+    int L;
+    __device__ uint32_t* hist(int p) const { return base + p * kBins0; }
+    __device__ uint32_t* coarse(int p) const { return base + kSegWgs * kBins0 + p * kCoarse; }
+    __device__ uint32_t* info(int p) const { return base + kSegWgs * (kBins0 + kCoarse) + 4 * p; }
+    __device__ uint32_t* cand_key() const { return info(kSegWgs); }
+};
+
+struct SegCoords {
+    int r, p, n, lo, hi, seg;
+};
+__device__ __forceinline__ SegCoords seg_coords(const int32_t* len, int L) {
+    SegCoords c;
+    c.r = blockIdx.x;
+    c.p = blockIdx.y;
+    c.n = min(max(len[c.r], 0), L);
+    c.seg = (c.n + kSegWgs - 1) / kSegWgs;
+    c.lo = min(c.p * c.seg, c.n);
+    c.hi = min(c.lo + c.seg, c.n);
+    return c;
+}
+
+__global__ __launch_bounds__(kSegThreads) void seg_hist_kernel(const float* __restrict__ logits,
+                                                               const int32_t* __restrict__ len,
+                                                               int32_t* __restrict__ out, uint32_t* __restrict__ ws,
+                                                               int L, int K) {
+    __shared__ uint32_t hist[kBins0];
+    const SegCoords c = seg_coords(len, L);
+    const int tid = threadIdx.x;
+    if (c.n <= K) {  // every candidate is selected
+        if (c.p == 0)
+            for (int j = tid; j < K; j += kSegThreads) out[(int64_t)c.r * K + j] = j < c.n ? j : -1;
+        return;
+    }
+    for (int i = tid; i < kBins0; i += kSegThreads) hist[i] = 0;
+    __syncthreads();
+    const Row row{__builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(logits + (int64_t)c.r * L), (short)0,
+                                                    c.n * 4, 0x00020000)};
+    for (int base = c.lo; base < c.hi; base += kSegKeys * kSegThreads) {
+        uint32_t k[kSegKeys];  // one batch of loads in flight
+#pragma unroll
+        for (int j = 0; j < kSegKeys; ++j) k[j] = row.key(base + j * kSegThreads + tid);
+#pragma unroll
+        for (int j = 0; j < kSegKeys; ++j)
+            if (base + j * kSegThreads + tid < c.hi) atomicAdd(&hist[k[j] >> 20], 1u);
+    }
+    __syncthreads();
+    const SegRow w{ws + c.r * seg_row_words(L), L};
+    uint4* dst = reinterpret_cast<uint4*>(w.hist(c.p));
+    for (int i = tid; i < kBins0 / 4; i += kSegThreads) dst[i] = reinterpret_cast<const uint4*>(hist)[i];
+    if (tid < kCoarse) {  // coarse bin tid = fine bins 64 tid .. 64 tid + 63
+        uint32_t sum = 0;
+        for (int b = 0; b < kBins0 / kCoarse; ++b) sum += hist[tid * (kBins0 / kCoarse) + b];
+        w.coarse(c.p)[tid] = sum;
+    }
+}
+
+__global__ __launch_bounds__(kSegThreads) void seg_cand_kernel(const float* __restrict__ logits,
+                                                               const int32_t* __restrict__ len,
+                                                               uint32_t* __restrict__ ws, int L, int K) {
+    __shared__ uint32_t tot[kSegThreads / 64];
+    __shared__ uint32_t word[3];
+    const SegCoords c = seg_coords(len, L);
+    if (c.n <= K) return;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const SegRow w{ws + c.r * seg_row_words(L), L};
+    if (tid == 0) word[2] = 0;  // this segment's candidate count
+    // this segment's first batch of keys, issued before the histogram reads
+    // (it does not depend on them)
+    const Row row{__builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(logits + (int64_t)c.r * L), (short)0,
+                                                    c.n * 4, 0x00020000)};
+    uint32_t k[kSegKeys];
+#pragma unroll
+    for (int j = 0; j < kSegKeys; ++j) k[j] = row.key(c.lo + j * kSegThreads + tid);
+    // bin0 in two steps over the row's segments: the coarse bin (key bits
+    // 31..26) holding the TOPK-th largest key, then the fine bin within it.
+    // Wave 0, lane l: bin 63 - l of each step, counted from the top.
+    if (tid < 64) {
+        uint32_t v[kSegWgs], sum = 0;
+#pragma unroll
+        for (int q = 0; q < kSegWgs; ++q) v[q] = w.coarse(q)[kCoarse - 1 - lane];
+#pragma unroll
+        for (int q = 0; q < kSegWgs; ++q) sum += v[q];
+        uint32_t above = wave_incl_scan(sum, lane) - sum;
+        const bool cross = above < (uint32_t)K && above + sum >= (uint32_t)K;  // one lane
+        const uint64_t m = __ballot(cross);
+        const int src = __builtin_ctzll(m);
+        const uint32_t cbin = (uint32_t)(kCoarse - 1 - src);
+        above = __shfl(above, src);
+#pragma unroll
+        for (int q = 0; q < kSegWgs; ++q) v[q] = w.hist(q)[cbin * (kBins0 / kCoarse) + (kBins0 / kCoarse - 1 - lane)];
+        sum = 0;
+#pragma unroll
+        for (int q = 0; q < kSegWgs; ++q) sum += v[q];
+        uint32_t above2 = above + wave_incl_scan(sum, lane) - sum;
+        if (above2 < (uint32_t)K && above2 + sum >= (uint32_t)K) {
+            word[0] = cbin * (kBins0 / kCoarse) + (kBins0 / kCoarse - 1 - lane);
+            word[1] = above2;
+        }
+    }
+    __syncthreads();
+    const uint32_t bin0 = word[0];
+    // this segment: count the entries above bin0, append the keys of those in
+    // bin0 to the segment's own candidate range
+    uint32_t* ck = w.cand_key() + c.lo;
+    uint32_t mine_above = 0;
+    for (int base = c.lo; base < c.hi; base += kSegKeys * kSegThreads) {
+        if (base > c.lo)
+#pragma unroll
+            for (int j = 0; j < kSegKeys; ++j) k[j] = row.key(base + j * kSegThreads + tid);
+#pragma unroll
+        for (int j = 0; j < kSegKeys; ++j) {
+            const int s = base + j * kSegThreads + tid;
+            mine_above += (s < c.hi && (k[j] >> 20) > bin0) ? 1u : 0u;
+            const bool hit = s < c.hi && (k[j] >> 20) == bin0;
+            const uint64_t m = __ballot(hit);
+            if (m) {  // wave-uniform
+                uint32_t at = 0;
+                if (lane == 0) at = atomicAdd(&word[2], (uint32_t)__popcll(m));
+                at = (uint32_t)__builtin_amdgcn_readfirstlane((int)at) + lane_rank(m);
+                if (hit) ck[at] = k[j];
+            }
+        }
+    }
+    mine_above = wave_sum(mine_above);
+    __syncthreads();  // tot is reused
+    if (lane == 0) tot[tid >> 6] = mine_above;
+    __syncthreads();
+    if (tid == 0) {
+        uint32_t a = 0;
+        for (int v = 0; v < kSegThreads / 64; ++v) a += tot[v];
+        *reinterpret_cast<uint4*>(w.info(c.p)) = uint4{a, word[2], bin0, (uint32_t)K - word[1]};
+    }
+}
+
+// Exclusive prefix (in thread order) and total over the workgroup of a
+// per-thread count.  Uses tot[kSegThreads / 64] of LDS.
+__device__ __forceinline__ void block_prefix(uint32_t c, uint32_t* tot, uint32_t& before, uint32_t& total) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t incl = wave_incl_scan(c, lane);
+    if (lane == 63) tot[wave] = incl;
+    __syncthreads();
+    before = incl - c;
+    total = 0;
+#pragma unroll
+    for (int w = 0; w < kSegThreads / 64; ++w) {
+        const uint32_t t = tot[w];
+        if (w < wave) before += t;
+        total += t;
+    }
+    __syncthreads();  // tot is rewritten by the next call
+}
+
+__global__ __launch_bounds__(kSegThreads) void seg_emit_kernel(const float* __restrict__ logits,
+                                                               const int32_t* __restrict__ len,
+                                                               int32_t* __restrict__ out,
+                                                               const uint32_t* __restrict__ ws, int L, int K) {
+    __shared__ uint32_t ck[kSegCandCap];
+    __shared__ uint32_t hist[kBins0];
+    __shared__ uint32_t gt[kSegWgs], eq[kSegWgs];
+    __shared__ uint32_t above[kSegWgs], cbase[kSegWgs + 1];
+    __shared__ uint32_t tot[kSegThreads / 64];
+    __shared__ uint32_t word[4];
+    const SegCoords c = seg_coords(len, L);
+    if (c.n <= K) return;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const SegRow w{const_cast<uint32_t*>(ws) + c.r * seg_row_words(L), L};
+    // One round trip: every segment's info, the first kWin candidates of every
+    // segment's range (read before their counts are known) and this
+    // segment's first batch of keys.
+    constexpr int kWin = 128;                             // candidates per segment
+    constexpr int kWinPer = kSegWgs * kWin / kSegThreads;  // window slots per thread
+    const Row row{__builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(logits + (int64_t)c.r * L), (short)0,
+                                                    c.n * 4, 0x00020000)};
+    uint32_t h[kSegKeys];
+#pragma unroll
+    for (int j = 0; j < kSegKeys; ++j) h[j] = row.key(c.lo + kSegKeys * tid + j);
+    uint4 info = uint4{0, 0, 0, 0};
+    if (tid < kSegWgs) info = *reinterpret_cast<const uint4*>(w.info(tid));
+    // slot m of this thread: segment wq, index wi
+    const int wq = tid / (kWin / kWinPer);
+    uint32_t win_k[kWinPer];
+#pragma unroll
+    for (int m = 0; m < kWinPer; ++m)
+        win_k[m] = w.cand_key()[min(wq * c.seg + (tid % (kWin / kWinPer)) + m * (kWin / kWinPer), L - 1)];
+    if (tid < kSegWgs) {  // every segment's (entries above bin0, candidate count), bin0 and the entries to take
+        above[tid] = info.x;
+        cbase[tid] = info.y;
+        if (tid == 0) {
+            word[0] = info.z;
+            word[1] = info.w;
+        }
+        gt[tid] = eq[tid] = 0;
+    }
+    for (int i = tid; i < kBins0; i += kSegThreads) hist[i] = 0;
+    __syncthreads();
+    const bool windows = __syncthreads_and(tid >= kSegWgs || info.y <= (uint32_t)kWin);
+    if (tid == 0) {  // candidate counts -> offsets of the compacted list
+        uint32_t acc = 0;
+        for (int q = 0; q < kSegWgs; ++q) {
+            const uint32_t n_q = cbase[q];
+            cbase[q] = acc;
+            acc += n_q;
+        }
+        cbase[kSegWgs] = acc;
+    }
+    __syncthreads();
+    const uint32_t bin0 = word[0];
+    uint32_t need = word[1];
+    const int ncand = (int)cbase[kSegWgs];
+    const bool in_lds = ncand <= kSegCandCap;
+    // candidate i lives in segment q's range: index q * seg + (i - cbase[q])
+    auto src_index = [&](int i) -> int {
+        int q = 0;
+#pragma unroll
+        for (int t = 1; t < kSegWgs; ++t) q += (uint32_t)i >= cbase[t] ? 1 : 0;
+        return q * c.seg + (i - (int)cbase[q]);
+    };
+    if (windows) {  // every candidate came with the first round trip
+        const uint32_t nq = cbase[wq + 1] - cbase[wq];
+#pragma unroll
+        for (int m = 0; m < kWinPer; ++m) {
+            const uint32_t wi = (uint32_t)(tid % (kWin / kWinPer) + m * (kWin / kWinPer));
+            if (wi < nq) ck[cbase[wq] + wi] = win_k[m];
+        }
+    } else if (in_lds) {
+        for (int i = tid; i < ncand; i += kSegThreads) ck[i] = w.cand_key()[src_index(i)];
+    }
+    __syncthreads();
+    // The candidates are read from LDS, or (more than kSegCandCap of them) from
+    // the workspace: two instantiations, so the LDS one holds no global load.
+    auto resolve = [&](auto from_lds) -> uint32_t {
+    constexpr bool kLds = decltype(from_lds)::value;
+    auto key_at = [&](int i) -> uint32_t {
+        if constexpr (kLds) return ck[i];
+        else return w.cand_key()[src_index(i)];
+    };
+
+    // ---- T: the need-th largest candidate key (all share bits 31..20 = bin0):
+    // bits 19..8 from a 4096-bin histogram, then bits 7..0 from 256 bins
+    for (int i = tid; i < ncand; i += kSegThreads) atomicAdd(&hist[(key_at(i) >> 8) & (kBins0 - 1)], 1u);
+    __syncthreads();
+    {
+        // thread tid owns bins kBins0 - 1 - 16 tid - j (j = 0..15), counted from the top
+        uint32_t cnt[16], mine = 0;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            cnt[j] = hist[kBins0 - 1 - 16 * tid - j];
+            mine += cnt[j];
+        }
+        uint32_t before, total;
+        block_prefix(mine, tot, before, total);
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            if (before < need && before + cnt[j] >= need) {  // exactly one (thread, j) crosses
+                word[2] = (uint32_t)(kBins0 - 1 - 16 * tid - j);
+                word[3] = before;
+            }
+            before += cnt[j];
+        }
+    }
+    __syncthreads();
+    const uint32_t pre24 = (bin0 << 12) | word[2];  // key bits 31..8 of T
+    need -= word[3];
+    if (tid < 256) hist[tid] = 0;
+    __syncthreads();
+    for (int i = tid; i < ncand; i += kSegThreads) {
+        const uint32_t u = key_at(i);
+        if ((u >> 8) == pre24) atomicAdd(&hist[u & 255u], 1u);
+    }
+    __syncthreads();
+    if (tid < 64) {  // four bins per lane from the top
+        uint32_t cc[4], sum = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            cc[j] = hist[255 - (4 * lane + j)];
+            sum += cc[j];
+        }
+        uint32_t a = wave_incl_scan(sum, lane) - sum;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            if (a < need && a + cc[j] >= need) word[2] = (uint32_t)(255 - (4 * lane + j));
+            a += cc[j];
+        }
+    }
+    __syncthreads();
+    const uint32_t thr = (pre24 << 8) | word[2];
+
+    // ---- per segment: candidates above T and equal to T (wave ballots); ties
+    // go to the lowest s
+    {
+        // The list holds the segments in order, so candidate i belongs to the
+        // segment q with cbase[q] <= i < cbase[q + 1].
+        uint32_t ngt[kSegWgs] = {};
+        for (int base = 0; base < ncand; base += kSegThreads) {
+            const int i = base + tid;
+            const uint32_t u = i < ncand ? key_at(i) : 0u;
+            int q = -1;
+            if (i < ncand) {
+                q = 0;
+#pragma unroll
+                for (int t = 1; t < kSegWgs; ++t) q += (uint32_t)i >= cbase[t] ? 1 : 0;
+                if (u == thr) atomicAdd(&eq[q], 1u);  // rare
+            }
+#pragma unroll
+            for (int qq = 0; qq < kSegWgs; ++qq) ngt[qq] += (uint32_t)__popcll(__ballot(q == qq && u > thr));
+        }
+        if (lane == 0)
+#pragma unroll
+            for (int qq = 0; qq < kSegWgs; ++qq)
+                if (ngt[qq]) atomicAdd(&gt[qq], ngt[qq]);
+    }
+    __syncthreads();
+    return thr;
+    };
+    const uint32_t thr = in_lds ? resolve(std::true_type{}) : resolve(std::false_type{});
+    if (tid == 0) {  // offsets: segments in order, ties to the earliest
+        uint32_t gt_all = 0;
+        for (int q = 0; q < kSegWgs; ++q) gt_all += gt[q];
+        uint32_t off = 0, left = word[1] - gt_all;  // entries equal to T to take
+        for (int q = 0; q < kSegWgs; ++q) {
+            const uint32_t take = min(eq[q], left);
+            left -= take;
+            if (q == c.p) {
+                word[2] = off;
+                word[3] = take;
+            }
+            off += above[q] + gt[q] + take;
+        }
+    }
+    __syncthreads();
+    uint32_t pos = word[2];
+    const uint32_t take = word[3];
+
+    // ---- this segment's selected s, ascending: kSegKeys consecutive entries per thread
+    int32_t* dst = out + (int64_t)c.r * K;
+    uint32_t ties = 0;
+    for (int base = c.lo; base < c.hi; base += kSegKeys * kSegThreads) {
+        const int s0 = base + kSegKeys * tid;
+        if (base > c.lo)
+#pragma unroll
+            for (int j = 0; j < kSegKeys; ++j) h[j] = row.key(s0 + j);
+        uint32_t gtm = 0, eqm = 0;
+#pragma unroll
+        for (int j = 0; j < kSegKeys; ++j) {
+            const bool ok = s0 + j < c.hi;
+            gtm |= (ok && h[j] > thr) ? 1u << j : 0u;
+            eqm |= (ok && h[j] == thr) ? 1u << j : 0u;
+        }
+        uint32_t selm = gtm, eq_total = 0;
+        if (__syncthreads_or(eqm != 0u)) {  // rare: ties in this batch
+            uint32_t eq_before;
+            block_prefix((uint32_t)__popc(eqm), tot, eq_before, eq_total);
+            uint32_t rank = ties + eq_before;
+#pragma unroll
+            for (int j = 0; j < kSegKeys; ++j)
+                if ((eqm >> j) & 1u) {
+                    if (rank < take) selm |= 1u << j;
+                    ++rank;
+                }
+        }
+        uint32_t sel_before, sel_total;
+        block_prefix((uint32_t)__popc(selm), tot, sel_before, sel_total);
+        uint32_t at = pos + sel_before;
+#pragma unroll
+        for (int j = 0; j < kSegKeys; ++j)
+            if ((selm >> j) & 1u) dst[at++] = s0 + j;
+        pos += sel_total;
+        ties += eq_total;
+    }
+}
+
 template <int HI, int KS>
 int launch_logits(const IndexerParams& p, dim3 grid, hipStream_t stream) {
     hipLaunchKernelGGL((indexer_logits_kernel<HI, KS>), grid, dim3(256), 0, stream, p);
@@ -676,6 +1082,22 @@ int launch_indexer_logits(const IndexerParams& p, hipStream_t stream) {
         if (p.ks == 4) return launch_logits<32, 4>(p, grid, stream);
     }
     return (int)hipErrorInvalidValue;
+}
+
+int64_t indexer_topk_ws_bytes(int rows, int L) {
+    if (rows > kSegMaxRows) return 0;
+    return (int64_t)rows * seg_row_words(L) * 4;
+}
+
+int launch_indexer_topk_seg(const float* logits, const int32_t* len, int32_t* indices, void* ws, int rows, int L,
+                            int topk, hipStream_t stream) {
+    uint32_t* w = static_cast<uint32_t*>(ws);
+    const dim3 grid((unsigned)rows, (unsigned)kSegWgs);
+    hipLaunchKernelGGL(seg_hist_kernel, grid, dim3(kSegThreads), 0, stream, logits, len, indices, w, L, topk);
+    hipLaunchKernelGGL(seg_cand_kernel, grid, dim3(kSegThreads), 0, stream, logits, len, w, L, topk);
+    hipLaunchKernelGGL(seg_emit_kernel, grid, dim3(kSegThreads), 0, stream, logits, len, indices,
+                       static_cast<const uint32_t*>(w), L, topk);
+    return (int)hipGetLastError();
 }
 
 int launch_indexer_topk(const float* logits, const int32_t* len, int32_t* indices, int rows, int L, int topk,

@@ -83,4 +83,13 @@ int launch_indexer_logits(const IndexerParams& p, hipStream_t stream);
 int launch_indexer_topk(const float* logits, const int32_t* len, int32_t* indices, int rows, int L, int topk,
                         hipStream_t stream);
 
+// Workspace bytes of the segmented selection (several workgroups per row, for
+// few rows); 0 when rows are too many for it to pay.
+int64_t indexer_topk_ws_bytes(int rows, int L);
+
+// The same selection, segmented: three launches over the workspace (any
+// contents on entry).
+int launch_indexer_topk_seg(const float* logits, const int32_t* len, int32_t* indices, void* ws, int rows, int L,
+                            int topk, hipStream_t stream);
+
 }  // namespace dsa

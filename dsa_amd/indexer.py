@@ -59,9 +59,12 @@ def indexer_logits(q_idx, k_idx, weights, lengths):
     return logits
 
 
-def indexer_topk(logits, lengths, topk: int):
+def indexer_topk(logits, lengths, topk: int, *, segmented: bool = True):
     """``indices [B, SQ, 1, topk]`` int32: per row the ``topk`` largest logits among
-    ``s < lengths`` (ties: lower ``s`` first), ascending, padded with -1."""
+    ``s < lengths`` (ties: lower ``s`` first), ascending, padded with -1.
+
+    With few rows (``B * SQ <= 32``) and ``segmented`` the selection splits every
+    row over 8 workgroups (three launches, same result bit for bit)."""
     if type(topk) is not int or topk <= 0:
         raise ValueError("topk must be a positive int")
     if logits.dim() != 3 or min(logits.shape) <= 0:
@@ -76,9 +79,17 @@ def indexer_topk(logits, lengths, topk: int):
     indices = torch.empty((batch, queries, 1, topk), device=device, dtype=torch.int32)
     stream = torch.cuda.current_stream(device).cuda_stream
     p = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    lib = _lib.load()
+    # few rows: the segmented selection (8 workgroups per row) over a scratch workspace
+    ws_bytes = lib.dsa_indexer_topk_ws_bytes(batch, queries, length, topk) if segmented else 0
     with torch.cuda.device(device):
-        rc = _lib.load().dsa_indexer_topk(p(logits), p(lengths), p(indices), batch, queries, length, topk,
-                                          ctypes.c_void_p(stream))
+        if ws_bytes > 0:
+            ws = torch.empty(ws_bytes, device=device, dtype=torch.uint8)
+            rc = lib.dsa_indexer_topk_ws(p(logits), p(lengths), p(indices), batch, queries, length, topk,
+                                         p(ws), ws_bytes, ctypes.c_void_p(stream))
+        else:
+            rc = lib.dsa_indexer_topk(p(logits), p(lengths), p(indices), batch, queries, length, topk,
+                                      ctypes.c_void_p(stream))
     _lib.check(rc, "dsa_indexer_topk")
     return indices
 

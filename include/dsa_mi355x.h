@@ -252,6 +252,20 @@ int dsa_indexer_logits(const uint16_t* q_idx, const uint16_t* k_idx, const float
 int dsa_indexer_topk(const float* logits, const int32_t* lengths, int32_t* indices,
                      int B, int SQ, int L, int TOPK, hipStream_t stream);
 
+/*
+ * dsa_indexer_topk with a workspace (no reference counterpart, like the
+ * indexer).  With few rows (B * SQ <= 32) one workgroup per row leaves most
+ * CUs idle; given `workspace` of at least dsa_indexer_topk_ws_bytes bytes
+ * (16-byte aligned, any contents), every row is split over 8 workgroups in
+ * three launches instead.  Same result bit for bit.  A NULL workspace, or a
+ * size query that returns 0 (many rows), selects dsa_indexer_topk's kernel.
+ */
+int64_t dsa_indexer_topk_ws_bytes(int B, int SQ, int L, int TOPK);
+
+int dsa_indexer_topk_ws(const float* logits, const int32_t* lengths, int32_t* indices,
+                        int B, int SQ, int L, int TOPK, void* workspace, int64_t workspace_bytes,
+                        hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

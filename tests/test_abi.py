@@ -23,7 +23,7 @@ def test_header_declares_the_expected_entry_points():
     assert declared_functions() == sorted(
         ["dsa_version", "dsa_last_error", "dsa_plan_for", "dsa_plan_check", "dsa_partial_elems",
          "dsa_fwd", "dsa_fwd_main", "dsa_fwd_opts", "dsa_fwd_main_opts", "dsa_plan_for_opts", "dsa_merge",
-         "dsa_indexer_logits", "dsa_indexer_topk"])
+         "dsa_indexer_logits", "dsa_indexer_topk", "dsa_indexer_topk_ws_bytes", "dsa_indexer_topk_ws"])
 
 
 def test_library_exports_every_declared_symbol():
@@ -184,6 +184,25 @@ def test_fp8_planner_keeps_to_narrow_variants(shape):
     assert lib.dsa_plan_for(*shape, 256, ctypes.byref(ref)) == 0
     assert lib.dsa_plan_for_opts(*shape, 256, None, ctypes.byref(plan)) == 0
     assert bytes(plan) == bytes(ref)
+
+
+def test_indexer_topk_workspace_sizes_and_checks():
+    lib = _lib.load()
+    # few rows: 8 workgroups per row, each row (8 x (4096 + 64) histogram bins + 8 x 4 + L words)
+    # rounded to 4 words
+    words = (8 * (4096 + 64) + 32 + 32768 + 3) // 4 * 4
+    assert lib.dsa_indexer_topk_ws_bytes(8, 1, 32768, 2048) == 8 * words * 4
+    assert lib.dsa_indexer_topk_ws_bytes(32, 1, 1000, 100) > 0
+    assert lib.dsa_indexer_topk_ws_bytes(64, 2, 65536, 2048) == 0   # many rows: one workgroup per row
+    assert lib.dsa_indexer_topk_ws_bytes(0, 1, 100, 10) == 0
+    fake = ctypes.c_void_p(1 << 20)
+    need = lib.dsa_indexer_topk_ws_bytes(2, 1, 1000, 100)
+    assert lib.dsa_indexer_topk_ws(fake, fake, fake, 2, 1, 1000, 100, fake, need - 1, None) < 0
+    assert b"workspace" in lib.dsa_last_error()
+    assert lib.dsa_indexer_topk_ws(fake, fake, fake, 2, 1, 1000, 100, ctypes.c_void_p((1 << 20) + 4), need,
+                                   None) < 0
+    assert b"aligned" in lib.dsa_last_error()
+    assert lib.dsa_indexer_topk_ws(None, fake, fake, 2, 1, 1000, 100, fake, need, None) < 0
 
 
 def test_indexer_entry_points_validate_before_any_launch():

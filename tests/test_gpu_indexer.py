@@ -82,11 +82,16 @@ TOPK_CASES = [
     ("signed zeros and -inf", 13, 1, 2, 5000, 1000, "zeros"),
     ("narrow values", 15, 2, 2, 20000, 2048, "narrow"),
     ("constant rows", 16, 1, 3, 3000, 700, "constant"),
+    # more first-digit candidates than the segmented path keeps in LDS (8192)
+    ("constant long rows", 17, 1, 2, 20000, 2048, "constant"),
+    ("32 rows", 18, 8, 4, 9000, 2048, None),      # the most rows the segmented path takes
+    ("64 rows", 19, 16, 4, 5000, 1024, None),     # one workgroup per row either way
 ]
 
 
+@pytest.mark.parametrize("segmented", [True, False], ids=["segmented", "one-wg-per-row"])
 @pytest.mark.parametrize("tag,seed,B,SQ,L,K,mode", TOPK_CASES, ids=[c[0] for c in TOPK_CASES])
-def test_indexer_topk_bit_exact(tag, seed, B, SQ, L, K, mode):
+def test_indexer_topk_bit_exact(tag, seed, B, SQ, L, K, mode, segmented):
     g = torch.Generator().manual_seed(seed)
     logits = torch.randn(B, SQ, L, generator=g)
     lengths = torch.randint(0, L + 3, (B, SQ), generator=g, dtype=torch.int32)
@@ -102,8 +107,8 @@ def test_indexer_topk_bit_exact(tag, seed, B, SQ, L, K, mode):
         logits = 1.0 + logits * 1e-6
     elif mode == "constant":
         logits = torch.full((B, SQ, L), 0.25)
-    print(f"[{tag}] launching B={B} SQ={SQ} L={L} K={K}", flush=True)
-    got = dsa_amd.indexer_topk(logits.cuda(), lengths.cuda(), K)
+    print(f"[{tag}] launching B={B} SQ={SQ} L={L} K={K} segmented={segmented}", flush=True)
+    got = dsa_amd.indexer_topk(logits.cuda(), lengths.cuda(), K, segmented=segmented)
     torch.cuda.synchronize()
     ref = O.indexer_topk_ref(logits, lengths, K)
     assert torch.equal(got.cpu(), ref), tag
