@@ -193,3 +193,45 @@ def test_fused_through_c_abi_with_caller_counters():
     for a, b, c in zip(fused, again, fallback):
         assert torch.equal(a, b) and torch.equal(a, c)
     _check_oracle("fused c-abi", *fused, O.reference(*data))
+
+
+def _growing_case(seed, B=1, SQ=2, H=128, L=4096, K=2048):
+    """kv rows ramp 0 -> 4 along L and the indices are sorted, so the scores
+    rise by far more than 2^64 along the slots: a workgroup's first tiles sit
+    far below its max and it recomputes its range (second pass)."""
+    g = torch.Generator().manual_seed(seed)
+    q = (1.0 + 0.1 * torch.randn(B, SQ, H, 512, generator=g)).bfloat16()
+    kv = (torch.linspace(0.0, 4.0, L).view(1, L, 1, 1) + 0.1 * torch.randn(B, L, 1, 512, generator=g)).bfloat16()
+    qr = (0.1 * torch.randn(B, SQ, H, 64, generator=g)).bfloat16()
+    kr = (0.1 * torch.randn(B, L, 1, 64, generator=g)).bfloat16()
+    ids = torch.stack([torch.randperm(L, generator=g)[:K].sort().values for _ in range(B * SQ)])
+    return q, kv, qr, kr, ids.view(B, SQ, 1, K).int().contiguous()
+
+
+def test_fused_with_second_pass():
+    data = _growing_case(12)
+    dev = [t.cuda() for t in data]
+    for cfg in (Tuning(16, 64, 4, kv_waves=4, mfma=16), Tuning(32, 64, 2, kv_waves=2, mfma=16)):
+        print(f"[fused second pass {cfg}] launching", flush=True)
+        two = dsa_amd.forward(*dev, config=cfg)
+        one = dsa_amd.forward(*dev, config=_fused(cfg))
+        torch.cuda.synchronize()
+        for a, b in zip(two, one):
+            assert torch.equal(a, b), cfg
+        _check_oracle(f"fused second pass {cfg}", *one, O.reference(*data))
+    _counters_zero()
+
+
+@pytest.mark.parametrize("K,split", [(100, 2), (2047, 3), (70, 2)])
+def test_fused_ragged_topk(K, split):
+    data = _case(40 + K, B=2, SQ=2, H=48, L=3000, K=K)
+    dev = [t.cuda() for t in data]
+    cfg = Tuning(16, 64, split, kv_waves=4, mfma=16)
+    print(f"[fused ragged K={K} split={split}] launching", flush=True)
+    two = dsa_amd.forward(*dev, config=cfg)
+    one = dsa_amd.forward(*dev, config=_fused(cfg))
+    torch.cuda.synchronize()
+    for a, b in zip(two, one):
+        assert torch.equal(a, b)
+    _check_oracle(f"fused ragged K={K}", *one, O.reference(*data))
+    _counters_zero()
