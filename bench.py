@@ -74,7 +74,7 @@ def algorithmic_units(shape, fp8=False):
 class Call:
     """One preallocated forward call through the C ABI."""
 
-    def __init__(self, data, config: Tuning, block_table=None, fp8=False):
+    def __init__(self, data, config: Tuning, block_table=None, fp8=False, uv_dim=0):
         self.data = data
         q = data[0]
         length = data[1].shape[1] if block_table is None else block_table.shape[1] * data[1].shape[1]
@@ -94,7 +94,7 @@ class Call:
         dev = q.device
         # Fused-merge plan: one launch per call, the main kernel merging in
         # its last workgroup per (token, head group) on these arrival counters.
-        self.fused = config.fused_merge and config.split > 1
+        self.fused = config.fused_merge and config.split > 1 and not uv_dim
         if self.fused:
             self.counters = torch.zeros(b * sq * (h // config.bm), device=dev, dtype=torch.int32)
             if self.opts is None:
@@ -112,6 +112,14 @@ class Call:
         p = lambda t: None if t is None else ctypes.c_void_p(t.data_ptr())  # noqa: E731
         self.args = [p(t) for t in data] + [p(self.out), p(self.mx), p(self.sm), p(self.po), p(self.pm), p(self.pl)]
         self.lib = _lib.load()
+        # W_UV projection after the attention: each call has its own weights
+        # (one layer's [H, dv, 512]), so rotating calls do not share them.
+        self.uv = uv_dim
+        if uv_dim:
+            gen = torch.Generator(device=dev).manual_seed(uv_dim + len(self.args))
+            self.w = (torch.randn((h, uv_dim, 512), generator=gen, device=dev) / 512 ** 0.5).bfloat16()
+            self.out_v = torch.empty((b, sq, h, uv_dim), device=dev, dtype=torch.bfloat16)
+            self.uv_args = (p(self.w), uv_dim * 512, p(self.out_v))
 
     def main(self, stream):
         b, sq, h, length, k = self.shape
@@ -127,9 +135,20 @@ class Call:
             _lib.check(rc, "dsa_fwd_main")
 
     def merge(self, stream):
+        b, sq, h, _, _ = self.shape
+        if self.uv:  # the second launch: merge + W_UV, or W_UV of the bf16 output
+            w, stride, out_v = self.uv_args
+            if self.po is not None and not self.fused:
+                rc = self.lib.dsa_merge_uv(self.args[8], self.args[9], self.args[10], w, stride, out_v,
+                                           self.args[6], self.args[7], b * sq, h, self.config.split, self.uv,
+                                           stream)
+            else:
+                rc = self.lib.dsa_project_uv(self.args[5], w, stride, out_v, b * sq, h, self.uv, stream)
+            if rc:
+                _lib.check(rc, "dsa_merge_uv / dsa_project_uv")
+            return
         if self.po is None or self.fused:
             return
-        b, sq, h, _, _ = self.shape
         rc = self.lib.dsa_merge(self.args[8], self.args[9], self.args[10], self.args[5], self.args[6],
                                 self.args[7], b * sq, h, self.config.split, stream)
         if rc:
@@ -282,11 +301,11 @@ def run(name, args):
         calls = []
         for i, d in enumerate(sets):
             pd, table = paged(d, args.paged, args.seed + i)
-            calls.append(Call(pd, config, block_table=table))
+            calls.append(Call(pd, config, block_table=table, uv_dim=args.uv))
             if i:  # set 0 stays for the CPU baseline
                 sets[i] = None
     else:
-        calls = [Call(d, config, fp8=args.fp8) for d in sets]
+        calls = [Call(d, config, fp8=args.fp8, uv_dim=args.uv) for d in sets]
     wall, main_us, merge_us, span_us = time_calls(calls, args.steps, args.warmup)
     _, warm_main, _, warm_span = time_calls(calls[:1], args.steps, args.warmup)
     gbytes, flops = algorithmic_units(shape, args.fp8)
@@ -334,9 +353,29 @@ def run(name, args):
             "mfma_TFLOPs_span": round(flops / (span_us * 1e-6) / 1e12, 2),
         },
     }
+    if args.uv:
+        line["w_uv"] = uv_line(shape, config, args.uv, merge_us)
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(name, sets[0], args.cpu_budget)
     return line
+
+
+def uv_line(shape, config, dv, uv_us):
+    """The W_UV launch of a call (the merge_us slot of the breakdown):
+    algorithmic HBM bytes = the weights once, the latent input (bf16 output,
+    or the FP32 split partials with their max and sum when the merge is in
+    the same launch), the bf16 result (and max and sum); all HBM-bound."""
+    b, sq, h, _, _ = shape
+    tokens = b * sq
+    merged = config.split > 1
+    weights = h * dv * 512 * 2
+    latent = tokens * config.split * h * (512 + 2) * 4 if merged else tokens * h * 512 * 2
+    out = tokens * h * dv * 2 + (tokens * h * 8 if merged else 0)
+    nbytes = weights + latent + out
+    gbps = nbytes / (uv_us * 1e-6) / 1e9
+    return {"kernel": "merge_uv" if merged else "project_uv", "dv": dv, "us": round(uv_us, 3),
+            "bytes": nbytes, "weight_bytes": weights, "GBps": round(gbps, 1),
+            "frac_hbm": round(gbps / HBM_PEAK_GBS, 4), "flops": 2 * tokens * h * dv * 512}
 
 
 # ---------------------------------------------------------------- indexer
@@ -495,6 +534,8 @@ def main():
                     help="run the workload on the fp8 kv row format (656 bytes per row)")
     ap.add_argument("--indexer", default="", metavar="WORKLOAD",
                     help="time the lightning indexer instead: " + ", ".join(INDEXER_CONFIGS) + " or all")
+    ap.add_argument("--uv", type=int, default=0, metavar="DV",
+                    help="append the W_UV output projection (value head dim DV, e.g. 128) to every call")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU oracle timing")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",

@@ -107,12 +107,37 @@ def _check_scale(scale):
     return scale
 
 
-def plan_call(shape, config=None, cores: int = 256, kv_fp8: bool = False):
+def _uv_launch(tokens: int, heads: int, dv: int, merge: bool) -> Launch:
+    """Launch descriptor of the W_UV kernel (mirrors project_uv.hip:uv_shape)."""
+    ndt = dv // 16
+
+    def d_shape(wgs):
+        nj = 2 if ndt % 8 == 0 and wgs * (ndt // 8) >= 256 else 1
+        return ndt // (4 * nj)
+
+    if merge:
+        nchunk = (tokens + 15) // 16
+        dsplit = d_shape(heads * nchunk)
+        return Launch("merge_uv", heads * nchunk * dsplit, 256, 16 * 1024)
+    tb = 32  # tokens per tile, four LDS buffers
+    ntiles = (tokens + tb - 1) // tb
+    dsplit = d_shape(heads * ntiles)
+    want = ((256 + heads - 1) // heads + dsplit - 1) // dsplit
+    per = (ntiles + want - 1) // want
+    nchunk = (ntiles + per - 1) // per
+    return Launch("project_uv", heads * nchunk * dsplit, 256, 4 * tb * 1024)
+
+
+def plan_call(shape, config=None, cores: int = 256, kv_fp8: bool = False, w_uv_dim: int | None = None):
     """Plan of one call: (Tuning, partial-buffer shapes or None, launches).
 
     Pure host logic (reference: dsa/api.py:88-113); usable without a GPU.
     ``kv_fp8``: the call reads fp8 kv rows, which only the narrow variants
-    (``mfma=16``) do.
+    (``mfma=16``) do.  ``w_uv_dim``: the value head dimension of a W_UV
+    projection that follows (no reference counterpart): a split plan then
+    merges and projects in one launch after the main kernel (its in-kernel
+    merge, if any, is not used: the W_UV launch is there anyway), a plan
+    without a split adds a projection launch.
     """
     if type(cores) is not int or cores <= 0:
         raise ValueError("cores must be a positive int")
@@ -128,10 +153,16 @@ def plan_call(shape, config=None, cores: int = 256, kv_fp8: bool = False):
     launches = [Launch(f"sparse_mla_fwd_{variant}_h{config.bm}_kw{config.kv_waves}_bn{config.bn}_s{config.stages}",
                        tokens * config.split * (heads // config.bm), 256, _LDS_BYTES)]
     partials = None
+    merged = False
     if config.split > 1:
         partials = ((batch, queries, config.split, heads, HEAD_DIM), (batch, queries, config.split, heads))
-        if not config.fused_merge:
+        if w_uv_dim is not None:
+            launches.append(_uv_launch(tokens, heads, w_uv_dim, True))
+            merged = True
+        elif not config.fused_merge:
             launches.append(Launch("merge_partials", tokens * ((heads + 1) // 2), 256, 0))
+    if w_uv_dim is not None and not merged:
+        launches.append(_uv_launch(tokens, heads, w_uv_dim, False))
     return config, partials, tuple(launches)
 
 
@@ -155,8 +186,64 @@ def _arrival_counters(device, stream: int, count: int) -> torch.Tensor:
         return buf
 
 
+def _check_w_uv(w_uv, heads: int, device):
+    """W_UV weights: bf16 ``[H, dv, 512]`` with unit strides in the last two
+    dims and any head stride (a multiple of 8 elements, at least dv * 512).
+    Returns ``(dv, head_stride)``."""
+    if not isinstance(w_uv, torch.Tensor) or w_uv.dim() != 3 or w_uv.shape[0] != heads \
+            or w_uv.shape[2] != HEAD_DIM:
+        raise ValueError(f"w_uv must be [H={heads}, dv, 512]")
+    dv = w_uv.shape[1]
+    if dv < 64 or dv > 256 or dv % 64:
+        raise ValueError(f"w_uv's dv must be a multiple of 64 in [64, 256] (got {dv})")
+    if w_uv.dtype != torch.bfloat16:
+        raise ValueError("w_uv must be bfloat16")
+    if w_uv.device != device:
+        raise ValueError("w_uv must be on the same ROCm GPU as the other inputs")
+    s0, s1, s2 = w_uv.stride()
+    if s2 != 1 or s1 != HEAD_DIM or (heads > 1 and (s0 < dv * HEAD_DIM or s0 % 8)) or w_uv.data_ptr() % 16:
+        raise ValueError("w_uv needs rows of 512 contiguous elements, 16-byte aligned, and a head stride "
+                         ">= dv * 512 that is a multiple of 8 (a slice of wkv_b's value rows qualifies)")
+    return dv, (s0 if heads > 1 else dv * HEAD_DIM)
+
+
+def _vp(t):
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def project_uv(output, w_uv):
+    """W_UV output projection of a latent attention output (no reference
+    counterpart; DeepSeek-V3.2-Exp inference/model.py, MLA.forward absorb
+    branch: ``einsum("bshc,hdc->bshd", x, wkv_b[:, -v_head_dim:])``).
+
+    ``output [..., H, 512]`` bf16 (contiguous, e.g. :func:`forward`'s) and
+    ``w_uv [H, dv, 512]`` bf16 (see :func:`forward`); returns bf16
+    ``[..., H, dv]``: ``out[t, h, d] = sum_c output[t, h, c] * w_uv[h, d, c]``
+    accumulated in fp32 and rounded once.
+    """
+    if output.dim() < 2 or output.shape[-1] != HEAD_DIM:
+        raise ValueError("output must be [..., H, 512]")
+    heads = output.shape[-2]
+    device = output.device
+    if device.type != "cuda" or torch.version.hip is None or not output.is_contiguous():
+        raise ValueError("output must be contiguous on a ROCm GPU")
+    if output.dtype != torch.bfloat16:
+        raise ValueError("output must be bfloat16")
+    dv, head_stride = _check_w_uv(w_uv, heads, device)
+    tokens = output.numel() // (heads * HEAD_DIM)
+    out_v = torch.empty((*output.shape[:-1], dv), device=device, dtype=torch.bfloat16)
+    if tokens == 0:
+        return out_v
+    stream = torch.cuda.current_stream(device).cuda_stream
+    with torch.cuda.device(device):
+        rc = _lib.load().dsa_project_uv(_vp(output), _vp(w_uv), head_stride, _vp(out_v), tokens, heads, dv,
+                                        ctypes.c_void_p(stream))
+    _lib.check(rc, "dsa_project_uv")
+    return out_v
+
+
 def forward(q, kv, q_rope, k_rope, indices, *, config=None, cores=None, return_kernels=False,
-            scale=None, block_table=None):
+            scale=None, block_table=None, w_uv=None):
     """Sparse MLA attention over given top-k indices.
 
     Returns ``(output, softmax_max, softmax_sum)``: bf16 ``[B,SQ,H,512]`` and
@@ -180,13 +267,22 @@ def forward(q, kv, q_rope, k_rope, indices, *, config=None, cores=None, return_k
     kv cache is a uint8 ``kv [B, L, 1, 656]`` (or pool) of rows written by
     :func:`dsa_amd.quantize_kv_fp8`, with ``k_rope=None``; the kernel computes
     with ``bf16(fp32(e4m3) * scale)`` latent values.
+
+    ``w_uv`` (bf16 ``[H, dv, 512]``, dv a multiple of 64 up to 256; heads may
+    be any stride apart, so ``wkv_b.view(H, d_nope + dv, 512)[:, -dv:]`` goes
+    in as it is) appends the W_UV output projection: the first result is then
+    bf16 ``[B,SQ,H,dv]`` = :func:`project_uv` of the latent output, bit for
+    bit.  With a split plan the merge runs in the W_UV launch (also for a
+    fused-merge plan: the main kernel then leaves its partials), and the
+    latent output is never written.
     """
     scale = _check_scale(scale)
     shape, device, fp8 = _check_inputs(q, kv, q_rope, k_rope, indices, block_table)
+    batch, queries, heads, length, topk = shape
+    uv = None if w_uv is None else _check_w_uv(w_uv, heads, device)
     if cores is None:
         cores = torch.cuda.get_device_properties(device).multi_processor_count
-    config, partials, launches = plan_call(shape, config, cores, fp8)
-    batch, queries, heads, length, topk = shape
+    config, partials, launches = plan_call(shape, config, cores, fp8, None if uv is None else uv[0])
 
     output = torch.empty_like(q)
     maximum = torch.empty((batch, 1, queries, heads), device=device, dtype=torch.float32)
@@ -206,9 +302,22 @@ def forward(q, kv, q_rope, k_rope, indices, *, config=None, cores=None, return_k
     args = (ptr(q), ptr(kv), ptr(q_rope), ptr(k_rope), ptr(indices),
             ptr(output), ptr(maximum), ptr(denominator), ptr(part_o), ptr(part_m), ptr(part_l),
             batch, queries, heads, length, topk)
-    fused = config.fused_merge and config.split > 1
+    merge_uv = uv is not None and config.split > 1
+    fused = config.fused_merge and config.split > 1 and not merge_uv
     with torch.cuda.device(device):
-        if scale is None and block_table is None and not fp8 and not fused:
+        if merge_uv:
+            # Main kernel only; the merge runs inside the W_UV launch below.
+            opts = _lib.DsaFwdOptions()
+            opts.scale = 0.0 if scale is None else scale
+            opts.kv_format = _lib.KV_FP8 if fp8 else _lib.KV_BF16
+            if block_table is not None:
+                opts.block_size = kv.shape[1]
+                opts.max_blocks = block_table.shape[1]
+                opts.num_blocks = kv.shape[0]
+                opts.block_table = block_table.data_ptr()
+            rc = _lib.load().dsa_fwd_main_opts(*args, ctypes.byref(opts), ctypes.byref(plan),
+                                               ctypes.c_void_p(stream))
+        elif scale is None and block_table is None and not fp8 and not fused:
             rc = _lib.load().dsa_fwd(*args, ctypes.byref(plan), ctypes.c_void_p(stream))
         else:
             opts = _lib.DsaFwdOptions()
@@ -223,19 +332,26 @@ def forward(q, kv, q_rope, k_rope, indices, *, config=None, cores=None, return_k
                 counters = _arrival_counters(device, stream, batch * queries * (heads // config.bm))
                 opts.arrivals = counters.data_ptr()
             rc = _lib.load().dsa_fwd_opts(*args, ctypes.byref(opts), ctypes.byref(plan), ctypes.c_void_p(stream))
-    _lib.check(rc, "dsa_fwd")
-    result = (output, maximum, denominator)
+    _lib.check(rc, "dsa_fwd_main" if merge_uv else "dsa_fwd")
+    if uv is None:
+        result = (output, maximum, denominator)
+    elif merge_uv:
+        dv, head_stride = uv
+        out_v = torch.empty((batch, queries, heads, dv), device=device, dtype=torch.bfloat16)
+        with torch.cuda.device(device):
+            rc = _lib.load().dsa_merge_uv(ptr(part_o), ptr(part_m), ptr(part_l), _vp(w_uv), head_stride,
+                                          _vp(out_v), ptr(maximum), ptr(denominator), batch * queries, heads,
+                                          config.split, dv, ctypes.c_void_p(stream))
+        _lib.check(rc, "dsa_merge_uv")
+        result = (out_v, maximum, denominator)
+    else:
+        result = (project_uv(output, w_uv), maximum, denominator)
     if return_kernels:
         return result, launches
     return result
 
 
-def merge(part_o, part_m, part_l):
-    """FP32 merge of split partials (reference: dsa/merge.py:13-91).
-
-    ``part_o [B,SQ,S,H,512]``, ``part_m``/``part_l [B,SQ,S,H]`` fp32 on one ROCm
-    GPU; returns ``(output, softmax_max, softmax_sum)`` as :func:`forward`.
-    """
+def _check_partials(part_o, part_m, part_l):
     if part_o.dim() != 5 or part_o.shape[-1] != HEAD_DIM:
         raise ValueError("part_o must be [B,SQ,S,H,512]")
     batch, queries, split, heads, _ = part_o.shape
@@ -248,6 +364,17 @@ def merge(part_o, part_m, part_l):
         raise ValueError("partials must be contiguous and on the same ROCm GPU")
     if any(t.dtype != torch.float32 for t in (part_o, part_m, part_l)):
         raise ValueError("partials must be float32")
+    return batch, queries, split, heads
+
+
+def merge(part_o, part_m, part_l):
+    """FP32 merge of split partials (reference: dsa/merge.py:13-91).
+
+    ``part_o [B,SQ,S,H,512]``, ``part_m``/``part_l [B,SQ,S,H]`` fp32 on one ROCm
+    GPU; returns ``(output, softmax_max, softmax_sum)`` as :func:`forward`.
+    """
+    batch, queries, split, heads = _check_partials(part_o, part_m, part_l)
+    device = part_o.device
     output = torch.empty((batch, queries, heads, HEAD_DIM), device=device, dtype=torch.bfloat16)
     maximum = torch.empty((batch, 1, queries, heads), device=device, dtype=torch.float32)
     denominator = torch.empty_like(maximum)
@@ -260,3 +387,23 @@ def merge(part_o, part_m, part_l):
             batch * queries, heads, split, ctypes.c_void_p(stream))
     _lib.check(rc, "dsa_merge")
     return output, maximum, denominator
+
+
+def merge_uv(part_o, part_m, part_l, w_uv):
+    """:func:`merge` and :func:`project_uv` in one launch (no reference
+    counterpart): returns ``(out_v [B,SQ,H,dv], softmax_max, softmax_sum)``,
+    bit-identical to ``project_uv(merge(...)[0], w_uv)`` and ``merge``'s
+    max and sum; the merged 512-wide rows are never written."""
+    batch, queries, split, heads = _check_partials(part_o, part_m, part_l)
+    device = part_o.device
+    dv, head_stride = _check_w_uv(w_uv, heads, device)
+    out_v = torch.empty((batch, queries, heads, dv), device=device, dtype=torch.bfloat16)
+    maximum = torch.empty((batch, 1, queries, heads), device=device, dtype=torch.float32)
+    denominator = torch.empty_like(maximum)
+    stream = torch.cuda.current_stream(device).cuda_stream
+    with torch.cuda.device(device):
+        rc = _lib.load().dsa_merge_uv(_vp(part_o), _vp(part_m), _vp(part_l), _vp(w_uv), head_stride, _vp(out_v),
+                                      _vp(maximum), _vp(denominator), batch * queries, heads, split, dv,
+                                      ctypes.c_void_p(stream))
+    _lib.check(rc, "dsa_merge_uv")
+    return out_v, maximum, denominator

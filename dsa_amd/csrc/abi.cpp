@@ -213,6 +213,57 @@ int dsa_merge(const float* part_o, const float* part_m, const float* part_l, uin
 
 namespace {
 
+// Shared checks of the W_UV entry points.
+int check_uv(const uint16_t* w_uv, int64_t w_head_stride, const uint16_t* out_v, int tokens, int H, int dv) {
+    if (!w_uv || !out_v) return fail(-1, "NULL pointer argument");
+    if (tokens <= 0 || H <= 0) return fail(-1, "tokens and H must be positive (got %d, %d)", tokens, H);
+    if (dv < 64 || dv > 256 || dv % 64)
+        return fail(-1, "dv must be a multiple of 64 in [64, 256] (got %d)", dv);
+    if (w_head_stride < (int64_t)dv * 512 || w_head_stride % 8)
+        return fail(-1, "w_head_stride must be a multiple of 8 and >= dv * 512 (got %lld)",
+                    (long long)w_head_stride);
+    if ((uintptr_t)w_uv & 15) return fail(-1, "w_uv must be 16-byte aligned");
+    if ((uintptr_t)out_v & 7) return fail(-1, "out_v must be 8-byte aligned");
+    // Workgroups: H * ceil(tokens / 16) at most, times a d-split of 4 at most;
+    // 32-bit byte offsets within 32 tokens of out_v.
+    if ((int64_t)H * ((tokens + 15) / 16) * 4 > INT32_MAX) return fail(-1, "tokens * H too large");
+    if ((int64_t)H * dv > (1 << 24)) return fail(-1, "H * dv too large (at most 2^24)");
+    return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+int dsa_project_uv(const uint16_t* output, const uint16_t* w_uv, int64_t w_head_stride, uint16_t* out_v,
+                   int tokens, int H, int dv, hipStream_t stream) {
+    if (!output) return fail(-1, "NULL pointer argument");
+    if (int rc = check_uv(w_uv, w_head_stride, out_v, tokens, H, dv)) return rc;
+    if ((uintptr_t)output & 15) return fail(-1, "output must be 16-byte aligned");
+    const int rc = dsa::launch_project_uv(output, w_uv, w_head_stride, out_v, tokens, H, dv, stream);
+    if (rc) return hip_fail(rc, "project_uv launch");
+    g_err[0] = 0;
+    return 0;
+}
+
+int dsa_merge_uv(const float* part_o, const float* part_m, const float* part_l, const uint16_t* w_uv,
+                 int64_t w_head_stride, uint16_t* out_v, float* out_max, float* out_sum, int tokens, int H,
+                 int split, int dv, hipStream_t stream) {
+    if (!part_o || !part_m || !part_l || !out_max || !out_sum) return fail(-1, "NULL pointer argument");
+    if (int rc = check_uv(w_uv, w_head_stride, out_v, tokens, H, dv)) return rc;
+    if (split <= 0) return fail(-1, "split must be positive (got %d)", split);
+    if ((uintptr_t)part_o & 15) return fail(-1, "part_o must be 16-byte aligned");
+    const int rc = dsa::launch_merge_uv(part_o, part_m, part_l, w_uv, w_head_stride, out_v, out_max, out_sum,
+                                        tokens, H, split, dv, stream);
+    if (rc) return hip_fail(rc, "merge_uv launch");
+    g_err[0] = 0;
+    return 0;
+}
+
+}  // extern "C"
+
+namespace {
+
 // Shared by dsa_fwd and dsa_fwd_main: validate, resolve the plan, launch the
 // main kernel and, when `with_merge` and split > 1, the merge.
 int fwd_impl(const uint16_t* q, const uint16_t* kv, const uint16_t* q_rope, const uint16_t* k_rope,

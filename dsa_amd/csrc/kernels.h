@@ -57,6 +57,16 @@ int launch_merge(const float* part_o, const float* part_m, const float* part_l,
                  uint16_t* out, float* out_max, float* out_sum,
                  int tokens, int H, int nsplit, hipStream_t stream);
 
+// Enqueue the W_UV projection of a bf16 latent output (project_uv.hip);
+// returns a hipError_t.
+int launch_project_uv(const uint16_t* lat, const uint16_t* w, int64_t w_head_stride, uint16_t* out_v,
+                      int tokens, int H, int dv, hipStream_t stream);
+
+// Enqueue the split merge fused with the W_UV projection; returns a hipError_t.
+int launch_merge_uv(const float* part_o, const float* part_m, const float* part_l, const uint16_t* w,
+                    int64_t w_head_stride, uint16_t* out_v, float* out_max, float* out_sum, int tokens,
+                    int H, int nsplit, int dv, hipStream_t stream);
+
 }  // namespace dsa
 
 namespace dsa {

@@ -3,9 +3,9 @@
 //   m = max_s m_s;  w_s = exp(m_s - m);  l = sum_s w_s * l_s;
 //   out = bf16(sum_s w_s * u_s / l);  out_max = m;  out_sum = l.
 // One workgroup merges two heads of one token; each thread owns 4 of the 512
-// columns and streams the split partials with 16-byte loads, kBatch splits in
-// flight at a time.  The arithmetic is merge_math.h's, which the main
-// kernel's in-kernel merge shares.
+// columns and streams the split partials with 16-byte loads, kMergeBatch
+// splits in flight at a time.  The arithmetic is merge_math.h's, which the
+// main kernel's in-kernel merge and the merge + W_UV kernel share.
 #include <hip/hip_runtime.h>
 #include <float.h>
 #include <stdint.h>
@@ -18,8 +18,6 @@ namespace {
 
 typedef merge_f32x4 f32x4;
 
-constexpr int kBatch = 16;  // split partials loaded per batch (kept in flight together)
-
 __global__ __launch_bounds__(256) void merge_kernel(const float* __restrict__ part_o,
                                                     const float* __restrict__ part_m,
                                                     const float* __restrict__ part_l,
@@ -31,43 +29,16 @@ __global__ __launch_bounds__(256) void merge_kernel(const float* __restrict__ pa
     const int h = (blockIdx.x % pairs) * 2 + (threadIdx.x >> 7);
     if (h >= H) return;
     const int col = (threadIdx.x & 127) * 4;
-    const int64_t base = (int64_t)token * nsplit * H + h;  // + s * H
-
-    // One pass: every batch's m, l and u are loaded together (a single round
-    // trip when nsplit <= kBatch, where the result is exactly the two-pass
-    // formula above); later batches fold in with the usual rescale.
-    float m = -FLT_MAX;
-    float l = 0.f;
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    for (int s0 = 0; s0 < nsplit; s0 += kBatch) {
-        f32x4 u[kBatch];
-        float ms[kBatch], ls[kBatch];
-#pragma unroll
-        for (int j = 0; j < kBatch; ++j) {
-            const bool live = s0 + j < nsplit;
-            const int64_t row = base + (int64_t)(live ? s0 + j : 0) * H;
-            ms[j] = live ? part_m[row] : -FLT_MAX;
-            ls[j] = live ? part_l[row] : 0.f;
-            u[j] = live ? *reinterpret_cast<const f32x4*>(part_o + row * 512 + col) : f32x4{0.f, 0.f, 0.f, 0.f};
-        }
-        float mb = m;
-#pragma unroll
-        for (int j = 0; j < kBatch; ++j) mb = fmaxf(mb, ms[j]);
-        if (s0 > 0) {
-            const float alpha = merge_weight(m, mb);
-            l *= alpha;
-            acc *= alpha;
-        }
-        m = mb;
-#pragma unroll
-        for (int j = 0; j < kBatch; ++j)
-            if (s0 + j < nsplit) merge_add(merge_weight(ms[j], m), ls[j], u[j], l, acc);
-    }
+    const int64_t base[1] = {(int64_t)token * nsplit * H + h};  // + s * H
+    const int cols[1] = {col};
+    f32x4 acc[1];
+    float m[1], l[1];
+    merge_units<1>(part_o, part_m, part_l, base, cols, H, nsplit, acc, m, l);
     const int64_t orow = (int64_t)token * H + h;
-    *reinterpret_cast<merge_bf16x4*>(out + orow * 512 + col) = merge_finish(acc, l);
+    *reinterpret_cast<merge_bf16x4*>(out + orow * 512 + col) = merge_finish(acc[0], l[0]);
     if ((threadIdx.x & 127) == 0) {
-        out_max[orow] = m;
-        out_sum[orow] = l;
+        out_max[orow] = m[0];
+        out_sum[orow] = l[0];
     }
 }
 

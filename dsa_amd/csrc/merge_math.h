@@ -41,6 +41,61 @@ __device__ __forceinline__ void merge_add_cols(float w, merge_f32x4 u_s, merge_f
     acc[3] = __builtin_fmaf(w, u_s[3], acc[3]);
 }
 
+// Split partials folded per batch of kMergeBatch: with nsplit <= kMergeBatch
+// the merge is one load round trip and exactly the formula above; later
+// batches fold in with a rescale by exp(m_old - m_new).  A caller that knows
+// nsplit <= BATCH < kMergeBatch may use the narrower BATCH: one batch either
+// way, the same operations (the max is exact, dead slots are -FLT_MAX and
+// never added), so the same bits.
+constexpr int kMergeBatch = 16;
+
+// The merge of NU (token, head) rows at 4 columns each: row r's partials are
+// part_o[(base[r] + s * H) * 512 + col[r] .. + 3], part_m / part_l[base[r] + s * H]
+// for s < nsplit.  Every load of a batch is issued before any arithmetic.
+// Returns the unnormalised sums in acc, with m and l.
+template <int NU, int BATCH = kMergeBatch>
+__device__ __forceinline__ void merge_units(const float* __restrict__ part_o, const float* __restrict__ part_m,
+                                            const float* __restrict__ part_l, const int64_t (&base)[NU],
+                                            const int (&col)[NU], int H, int nsplit, merge_f32x4 (&acc)[NU],
+                                            float (&m)[NU], float (&l)[NU]) {
+#pragma unroll
+    for (int r = 0; r < NU; ++r) {
+        m[r] = -FLT_MAX;
+        l[r] = 0.f;
+        acc[r] = merge_f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    for (int s0 = 0; s0 < nsplit; s0 += BATCH) {
+        merge_f32x4 u[NU][BATCH];
+        float ms[NU][BATCH], ls[NU][BATCH];
+#pragma unroll
+        for (int r = 0; r < NU; ++r)
+#pragma unroll
+            for (int j = 0; j < BATCH; ++j) {
+                const bool live = s0 + j < nsplit;
+                const int64_t row = base[r] + (int64_t)(live ? s0 + j : 0) * H;
+                ms[r][j] = live ? part_m[row] : -FLT_MAX;
+                ls[r][j] = live ? part_l[row] : 0.f;
+                u[r][j] = live ? *reinterpret_cast<const merge_f32x4*>(part_o + row * 512 + col[r])
+                               : merge_f32x4{0.f, 0.f, 0.f, 0.f};
+            }
+#pragma unroll
+        for (int r = 0; r < NU; ++r) {
+            float mb = m[r];
+#pragma unroll
+            for (int j = 0; j < BATCH; ++j) mb = fmaxf(mb, ms[r][j]);
+            if (s0 > 0) {
+                const float alpha = merge_weight(m[r], mb);
+                l[r] *= alpha;
+                acc[r] *= alpha;
+            }
+            m[r] = mb;
+#pragma unroll
+            for (int j = 0; j < BATCH; ++j)
+                if (s0 + j < nsplit) merge_add(merge_weight(ms[r][j], m[r]), ls[r][j], u[r][j], l[r], acc[r]);
+        }
+    }
+}
+
 __device__ __forceinline__ merge_bf16x4 merge_finish(merge_f32x4 acc, float l) {
     merge_bf16x4 o;
     o[0] = (__bf16)(acc[0] / l);

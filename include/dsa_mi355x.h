@@ -229,6 +229,40 @@ int dsa_merge(const float* part_o, const float* part_m, const float* part_l,
               int tokens, int H, int split, hipStream_t stream);
 
 /*
+ * W_UV output projection: the step after the attention (no reference
+ * counterpart; the reference stops at the 512-wide latent output and leaves
+ * the model's own scale and projections to the caller, README.md:81-83,
+ * FAIRNESS_AUDIT.md:28).  In MLA's absorbed form each head's latent output
+ * goes through that head's slice of the kv up-projection
+ * (DeepSeek-V3.2-Exp inference/model.py, MLA.forward:
+ * x = einsum("bshc,hdc->bshd", x, wkv_b[:, -v_head_dim:])):
+ *
+ *   out_v[t, h, d] = bf16( sum_{c < 512} output[t, h, c] * w_uv[h * w_head_stride + d * 512 + c] )
+ *
+ *   output [tokens, H, 512] bf16 (dsa_fwd's output, 16-byte aligned)
+ *   w_uv   bf16 rows of 512, dv rows per head, heads w_head_stride elements
+ *          apart (>= dv * 512, a multiple of 8; 16-byte aligned) -- so the
+ *          value rows of wkv_b viewed as [H, d_nope + dv, 512] go in as they
+ *          are, with w_head_stride = (d_nope + dv) * 512
+ *   out_v  [tokens, H, dv] bf16 (8-byte aligned); dv a multiple of 64 in [64, 256]
+ * FP32 accumulation, one bf16 rounding.
+ */
+int dsa_project_uv(const uint16_t* output, const uint16_t* w_uv, int64_t w_head_stride,
+                   uint16_t* out_v, int tokens, int H, int dv, hipStream_t stream);
+
+/*
+ * dsa_merge and dsa_project_uv in one launch (no reference counterpart):
+ * the merged 512-wide rows stay on chip and are never written.  out_v,
+ * out_max and out_sum are bit-identical to dsa_merge followed by
+ * dsa_project_uv.  part_o/part_m/part_l as for dsa_merge; w_uv, out_v, dv
+ * as for dsa_project_uv.
+ */
+int dsa_merge_uv(const float* part_o, const float* part_m, const float* part_l,
+                 const uint16_t* w_uv, int64_t w_head_stride, uint16_t* out_v,
+                 float* out_max, float* out_sum, int tokens, int H, int split, int dv,
+                 hipStream_t stream);
+
+/*
  * Lightning indexer: the token selector that produces `idx` for dsa_fwd (the
  * step before the attention; no reference counterpart -- the reference takes
  * the indices as an input, README.md:19-21).

@@ -40,6 +40,13 @@ Functions and the reference code each one restates:
                          the selection keeps the TOPK largest (ties: lower s)
                          in ascending s, -1 padded.
 
+* ``project_uv_ref``  -- the W_UV output projection after the attention (no
+                         reference counterpart: the reference stops at the
+                         latent output, README.md:81-83): DeepSeek-V3.2-Exp
+                         inference/model.py, MLA.forward absorb branch,
+                         ``einsum("bshc,hdc->bshd", x, wkv_b[:, -v_head_dim:])``,
+                         in FP64.
+
 ``reference(scale=...)`` generalises the fixed 1/24 (tools/review.py:140) to
 another softmax scale; the default keeps the reference's exact division.
 
@@ -53,6 +60,9 @@ FP8 rows: ``e4m3_decode`` against torch's float8_e4m3fn on all 256 codes and
 against hand-worked values; ``dequant_fp8_rows`` against an element-wise
 restatement, with planted mistakes (a 64-dim scale block, rounding to bf16
 before the scale) rejected.
+W_UV: an FP64 triple-loop brute force, one-hot weight rows (the projection
+then gathers latent columns exactly) and linearity, with planted mistakes
+(weights of the wrong head, the transposed head matrix) rejected.
 Indexer: FP64 brute-force logits (planted: ReLU or head weights dropped),
 brute-force selection over tie-heavy rows, -0.0 / +0.0, -inf and short rows
 (planted: ties taken from the top), and the float-key order.
@@ -186,6 +196,16 @@ def indexer_logits_ref(q_idx, k_idx, weights, lengths, chunk: int = 64):
     cols = torch.arange(length)
     out.masked_fill_(cols[None, None, :] >= lengths.clamp(0, length)[..., None].long(), -float("inf"))
     return out
+
+
+def project_uv_ref(output, w_uv):
+    """FP64 W_UV projection ``out[..., h, d] = sum_c output[..., h, c] *
+    w_uv[h, d, c]`` (DeepSeek-V3.2-Exp inference/model.py, MLA.forward:
+    ``einsum("bshc,hdc->bshd", x, wkv_b[:, -v_head_dim:])``); ``output
+    [..., H, 512]``, ``w_uv [H, dv, 512]``; returns float64 ``[..., H, dv]``."""
+    x = output.detach().cpu().double()
+    w = w_uv.detach().cpu().double()
+    return (x.unsqueeze(-2) * w).sum(-1)
 
 
 def float_key(values):

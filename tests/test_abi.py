@@ -23,7 +23,8 @@ def test_header_declares_the_expected_entry_points():
     assert declared_functions() == sorted(
         ["dsa_version", "dsa_last_error", "dsa_plan_for", "dsa_plan_check", "dsa_partial_elems",
          "dsa_fwd", "dsa_fwd_main", "dsa_fwd_opts", "dsa_fwd_main_opts", "dsa_plan_for_opts", "dsa_merge",
-         "dsa_indexer_logits", "dsa_indexer_topk", "dsa_indexer_topk_ws_bytes", "dsa_indexer_topk_ws"])
+         "dsa_indexer_logits", "dsa_indexer_topk", "dsa_indexer_topk_ws_bytes", "dsa_indexer_topk_ws",
+         "dsa_project_uv", "dsa_merge_uv"])
 
 
 def test_library_exports_every_declared_symbol():
@@ -221,3 +222,29 @@ def test_indexer_entry_points_validate_before_any_launch():
     assert b"query groups" in lib.dsa_last_error()
     assert lib.dsa_indexer_topk(fake, fake, fake, 1 << 11, 1 << 11, 100, 10, None) < 0
     assert b"4194304" in lib.dsa_last_error()
+
+
+def test_w_uv_entry_points_validate_before_any_launch():
+    lib = _lib.load()
+    fake = ctypes.c_void_p(1 << 20)
+    stride = 128 * 512
+    assert lib.dsa_project_uv(None, fake, stride, fake, 8, 16, 128, None) < 0
+    assert lib.dsa_project_uv(fake, fake, stride, fake, 0, 16, 128, None) < 0
+    for dv in (0, 32, 100, 320):
+        assert lib.dsa_project_uv(fake, fake, stride, fake, 8, 16, dv, None) < 0
+        assert b"dv" in lib.dsa_last_error()
+    assert lib.dsa_project_uv(fake, fake, stride - 8, fake, 8, 16, 128, None) < 0    # heads overlap
+    assert lib.dsa_project_uv(fake, fake, stride + 4, fake, 8, 16, 128, None) < 0    # not 16-byte rows
+    assert b"w_head_stride" in lib.dsa_last_error()
+    assert lib.dsa_project_uv(fake, ctypes.c_void_p((1 << 20) + 8), stride, fake, 8, 16, 128, None) < 0
+    assert lib.dsa_project_uv(fake, fake, stride, ctypes.c_void_p((1 << 20) + 2), 8, 16, 128, None) < 0
+    assert lib.dsa_project_uv(ctypes.c_void_p((1 << 20) + 8), fake, stride, fake, 8, 16, 128, None) < 0
+    assert b"aligned" in lib.dsa_last_error()
+    assert lib.dsa_project_uv(fake, fake, stride, fake, 1 << 30, 1 << 10, 128, None) < 0
+    assert lib.dsa_project_uv(fake, fake, 256 * 512, fake, 8, 1 << 17, 256, None) < 0
+    assert b"H * dv" in lib.dsa_last_error()
+    assert lib.dsa_merge_uv(fake, fake, None, fake, stride, fake, fake, fake, 8, 16, 2, 128, None) < 0
+    assert lib.dsa_merge_uv(fake, fake, fake, fake, stride, fake, fake, fake, 8, 16, 0, 128, None) < 0
+    assert lib.dsa_merge_uv(fake, fake, fake, fake, stride, fake, fake, fake, 8, 16, 2, 96, None) < 0
+    assert lib.dsa_merge_uv(ctypes.c_void_p((1 << 20) + 4), fake, fake, fake, stride, fake, fake, fake,
+                            8, 16, 2, 128, None) < 0

@@ -11,6 +11,7 @@ import torch
 
 import dsa_amd
 from dsa_amd import CASE_SHAPES, SELECTED, Tuning, plan_call
+from dsa_amd import api as A
 from dsa_amd.api import _check_inputs
 from dsa_amd.config import check_tuning, plan_for
 from dsa_amd.workloads import BASELINE_CONFIGS
@@ -287,3 +288,47 @@ def test_quantize_kv_fp8_rows():
         dsa_amd.quantize_kv_fp8(kv.float(), kr)
     with pytest.raises(ValueError):
         dsa_amd.quantize_kv_fp8(kv, kr[..., :32])
+
+
+def test_plan_call_w_uv_launches():
+    # split without the in-kernel merge: the merge runs inside the W_UV launch
+    cfg = Tuning(32, 64, 8, kv_waves=2, mfma=16)
+    _, partials, launches = A.plan_call((8, 1, 128, 32768, 2048), cfg, w_uv_dim=128)
+    assert partials is not None
+    assert [l.name for l in launches][1:] == ["merge_uv"]
+    assert launches[1].grid == 128 * 2 and launches[1].lds_bytes == 16 * 1024   # d split in 2
+    # a fused-merge plan also merges in the W_UV launch; no split: a projection follows
+    _, _, launches = A.plan_call((64, 2, 16, 65536, 2048), Tuning(16, 64, 2, kv_waves=4, mfma=16, fused_merge=True),
+                                 w_uv_dim=128)
+    assert [l.name for l in launches][1:] == ["merge_uv"]
+    _, _, launches = A.plan_call((1, 4096, 128, 32768, 2048), Tuning(128, 32, 1, stages=4), w_uv_dim=128)
+    assert [l.name for l in launches][1:] == ["project_uv"]
+    # prefill: two chunks of 2048 tokens per head, 32-token tiles in four LDS buffers
+    _, _, launches = A.plan_call((1, 4096, 128, 32768, 2048), Tuning(128, 32, 1, stages=4), w_uv_dim=128)
+    assert launches[1].grid == 128 * 2 and launches[1].lds_bytes == 4 * 32 * 1024
+    _, _, launches = A.plan_call((1, 4096, 16, 8192, 2048), None, w_uv_dim=128)
+    assert launches[-1].grid == 16 * 16
+    # 128 tokens, 256-wide values, split plan: 8 blocks of 16 tokens, d split in 2
+    _, _, launches = A.plan_call((64, 2, 16, 65536, 2048), None, w_uv_dim=256)
+    assert launches[-1].name == "merge_uv" and launches[-1].grid == 16 * 8 * 2
+    # the same without a split: 4 chunks of one 32-token tile, d split in 4
+    _, _, launches = A.plan_call((64, 2, 16, 65536, 2048), Tuning(16, 64, 1, kv_waves=4, mfma=16), w_uv_dim=256)
+    assert launches[-1].grid == 16 * 4 * 4 and launches[-1].lds_bytes == 4 * 32 * 1024
+
+
+@pytest.mark.parametrize("mutate,msg", [
+    (lambda w: w[:, :100], "multiple of 64"),
+    (lambda w: w[:8], "w_uv must be"),
+    (lambda w: w.float(), "bfloat16"),
+    (lambda w: w.transpose(1, 2)[:, :128, :], "w_uv must be"),
+    (lambda w: w[:, :, :].as_strided((16, 64, 512), (64 * 512 + 4, 512, 1)), "head stride"),
+], ids=["dv", "heads", "dtype", "transposed", "stride"])
+def test_w_uv_rejections(mutate, msg):
+    w = torch.zeros(16, 128, 512, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match=msg):
+        A._check_w_uv(mutate(w), 16, torch.device("cpu"))
+
+
+def test_w_uv_strided_value_rows_accepted():
+    wkv_b = torch.zeros(16, 128 + 128, 512, dtype=torch.bfloat16)
+    assert A._check_w_uv(wkv_b[:, -128:], 16, torch.device("cpu")) == (128, 256 * 512)

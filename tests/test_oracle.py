@@ -448,3 +448,48 @@ def test_dequant_fp8_planted_mistakes_are_caught():
     assert not torch.equal(coarse, kv)
     wrong_rope = rows[..., 464:592].contiguous().view(torch.bfloat16)
     assert not torch.equal(wrong_rope, rp)
+
+
+# --- W_UV output projection -------------------------------------------------
+
+def _uv_brute(x, w):
+    """Triple loop over (token, head, d) with a Python sum over c."""
+    xs, ws = x.double().tolist(), w.double().tolist()
+    tokens, heads = len(xs), len(xs[0])
+    dv = len(ws[0])
+    return torch.tensor([[[math.fsum(a * b for a, b in zip(xs[t][h], ws[h][d])) for d in range(dv)]
+                          for h in range(heads)] for t in range(tokens)], dtype=torch.float64)
+
+
+def test_project_uv_matches_brute_force():
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(3, 4, 512, generator=g).bfloat16()
+    w = torch.randn(4, 6, 512, generator=g).bfloat16()
+    torch.testing.assert_close(O.project_uv_ref(x, w), _uv_brute(x, w), rtol=1e-12, atol=1e-9)
+
+
+def test_project_uv_one_hot_rows_gather_columns():
+    # w[h, d, c] = 1 at c = (37 d + 11 h) % 512: out[t, h, d] is exactly x[t, h, c]
+    tokens, heads, dv = 5, 3, 64
+    x = torch.randn(tokens, heads, 512, generator=torch.Generator().manual_seed(6)).bfloat16()
+    w = torch.zeros(heads, dv, 512, dtype=torch.bfloat16)
+    cols = torch.tensor([[(37 * d + 11 * h) % 512 for d in range(dv)] for h in range(heads)])
+    for h in range(heads):
+        w[h, torch.arange(dv), cols[h]] = 1
+    out = O.project_uv_ref(x, w)
+    expect = torch.stack([x[:, h, cols[h]] for h in range(heads)], 1).double()
+    assert torch.equal(out, expect)
+
+
+def test_project_uv_linear_and_planted_mistakes_caught():
+    g = torch.Generator().manual_seed(7)
+    x1, x2 = (torch.randn(4, 3, 512, generator=g).double() for _ in range(2))
+    w = torch.randn(3, 64, 512, generator=g).double()
+    torch.testing.assert_close(O.project_uv_ref(2 * x1 - x2, w),
+                               2 * O.project_uv_ref(x1, w) - O.project_uv_ref(x2, w))
+    ref = _uv_brute(x1, w)
+    wrong_head = O.project_uv_ref(x1, w.roll(1, 0))
+    # the transposed head matrix (dv = 512 so the shapes still agree)
+    wt = torch.randn(3, 512, 512, generator=g).double()
+    assert (wrong_head - ref).abs().max() > 1.0
+    assert (O.project_uv_ref(x1, wt.transpose(1, 2)) - _uv_brute(x1, wt)).abs().max() > 1.0
