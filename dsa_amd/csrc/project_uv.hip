@@ -282,8 +282,9 @@ template <int NJ, int BATCH>
 __global__ __launch_bounds__(kThreads) void merge_uv_kernel(UvArgs a) {
     constexpr int TB = 16;
     // Units of 4 columns per thread per pass: the split loads of a pass in
-    // registers stay near 128 VGPRs (64 with the second weight tile).
-    constexpr int BUDGET = NJ == 2 ? 16 : 32;
+    // registers stay near 128 VGPRs (64 with the second weight tile; 96 for
+    // BATCH 4, whose weights-per-unit bookkeeping would spill at 128).
+    constexpr int BUDGET = NJ == 2 ? 16 : BATCH == 4 ? 24 : 32;
     constexpr int NU = BUDGET / BATCH < 1 ? 1 : BUDGET / BATCH < 8 ? BUDGET / BATCH : 8;
     __shared__ __attribute__((aligned(16))) uint8_t tile[TB * 1024];
     int h, blk, dp;
@@ -292,7 +293,6 @@ __global__ __launch_bounds__(kThreads) void merge_uv_kernel(UvArgs a) {
     const int ntok = min(TB, a.T - t0);
 
     bf16x8 wf[NJ][kKSteps];
-    load_weights<NJ>(wf, a, h, dp);
 
     // Units of 4 columns: 128 per token row.  Rows past ntok are left
     // unwritten: they feed only the D columns of tokens that are never
@@ -344,6 +344,9 @@ __global__ __launch_bounds__(kThreads) void merge_uv_kernel(UvArgs a) {
                                            : f32x4{0.f, 0.f, 0.f, 0.f};
         };
         if (q0 < units) load_u();
+        // The weights are needed only by the MFMAs: issued after the merge's
+        // loads, they stream while the merge is folded.
+        load_weights<NJ>(wf, a, h, dp);
         if (t < ntok) {
             float m = -FLT_MAX;
 #pragma unroll
@@ -362,7 +365,7 @@ __global__ __launch_bounds__(kThreads) void merge_uv_kernel(UvArgs a) {
                 a.out_sum[orow] = l;
             }
         }
-        __syncthreads();
+        lds_barrier();
         for (; q0 < units; q0 += NU * kThreads) {
             if (q0 != (int)threadIdx.x) load_u();
 #pragma unroll
@@ -376,6 +379,7 @@ __global__ __launch_bounds__(kThreads) void merge_uv_kernel(UvArgs a) {
             }
         }
     } else {
+        load_weights<NJ>(wf, a, h, dp);
         for (int q0 = threadIdx.x; q0 < units; q0 += NU * kThreads) {
             int64_t base[NU];
             int col[NU];
@@ -395,7 +399,7 @@ __global__ __launch_bounds__(kThreads) void merge_uv_kernel(UvArgs a) {
             }
         }
     }
-    __syncthreads();
+    lds_barrier();
     f32x4 acc[NJ][1];
     mma_tile<1, NJ>(tile, wf, acc);
     const int tt = threadIdx.x & 15;
