@@ -46,7 +46,7 @@ def _indices(g, B, SQ, K, L):
     return ids.contiguous()
 
 
-def _compact(rows_of_batch, ids, L):
+def _compact(ids, L):
     """Renumber each batch's selected rows 0..n-1: returns the row lists and
     the relabelled indices (-1 for every masked slot)."""
     B = ids.shape[0]
@@ -76,7 +76,7 @@ def test_max_length_contiguous(H, config):
     B, SQ, K, L = 2, 2, 1024, L_MAX
     g = torch.Generator().manual_seed(H)
     ids = _indices(g, B, SQ, K, L)
-    sel, ids_small = _compact(None, ids, L)
+    sel, ids_small = _compact(ids, L)
     nmax = max(int(s.numel()) for s in sel)
     kv_small = torch.zeros(B, nmax, 1, 512).bfloat16()
     kr_small = torch.zeros(B, nmax, 1, 64).bfloat16()
