@@ -37,10 +37,9 @@
 //   B fragments are read from LDS in groups of 8, one group ahead of the
 //   MFMAs that use them.
 // * merge_uv_kernel<NJ, BATCH>: workgroup = (head, 16 tokens, d part).  The
-//   weights are loaded first, so their stream overlaps the merge; the merge
-//   fills the tile with 32 / BATCH (16 / BATCH with two weight tiles; 1 to 8)
-//   units of 4 columns per thread per pass, every split load of a pass in
-//   flight at once.
+//   merge fills the tile with 32 / BATCH (16 / BATCH with two weight tiles;
+//   1 to 8) units of 4 columns per thread per pass, every split load of a
+//   pass in flight at once, the batch width matched to the split count.
 //
 // LDS tile: TB latent rows of 1 KiB; 16-byte chunk c of row t sits at chunk
 // c ^ (t & 15), so the 16 rows one B-operand read touches hit distinct banks.
@@ -310,92 +309,25 @@ __global__ __launch_bounds__(kThreads) void merge_uv_kernel(UvArgs a) {
         const int q = q0 + r * kThreads, c = q & 127;
         if (q < units) *reinterpret_cast<merge_bf16x4*>(tile + tile_off(q >> 7, c >> 1) + ((c & 1) << 3)) = o;
     };
-    if (a.nsplit <= BATCH) {
-        // One batch.  The token's max, weights and sum are the same for its
-        // 128 units: threads [0, ntok) fold them once into LDS (their m / l
-        // loads issued first, then everyone's first-pass u loads), and the
-        // units then only fold u.  The operations per value are those of
-        // merge_units, so the bits are.
-        __shared__ float wts[TB][BATCH];
-        __shared__ float lsum[TB];
-        const int t = threadIdx.x;
-        float msv[BATCH], lsv[BATCH];
-        if (t < ntok) {
-            const int64_t rb = (int64_t)(t0 + t) * a.nsplit * a.H + h;
+    // Every thread folds its own units' max, weights and sum (the same for the
+    // 128 units of a row): a per-row fold into LDS behind one thread measured
+    // slower, its barrier sitting in the merge's critical path.
+    load_weights<NJ>(wf, a, h, dp);
+    for (int q0 = threadIdx.x; q0 < units; q0 += NU * kThreads) {
+        int64_t base[NU];
+        int col[NU];
+        unit_rows(q0, base, col);
+        f32x4 acc[NU];
+        float m[NU], l[NU];
+        merge_units<NU, BATCH>(a.part_o, a.part_m, a.part_l, base, col, a.H, a.nsplit, acc, m, l);
 #pragma unroll
-            for (int j = 0; j < BATCH; ++j) {
-                const bool live = j < a.nsplit;
-                msv[j] = live ? a.part_m[rb + (int64_t)j * a.H] : -FLT_MAX;
-                lsv[j] = live ? a.part_l[rb + (int64_t)j * a.H] : 0.f;
-            }
-        }
-        int q0 = threadIdx.x;
-        f32x4 u[NU][BATCH];
-        auto load_u = [&]() {
-            int64_t base[NU];
-            int col[NU];
-            unit_rows(q0, base, col);
-#pragma unroll
-            for (int r = 0; r < NU; ++r)
-#pragma unroll
-                for (int j = 0; j < BATCH; ++j)
-                    u[r][j] = j < a.nsplit ? *reinterpret_cast<const f32x4*>(
-                                                 a.part_o + (base[r] + (int64_t)j * a.H) * 512 + col[r])
-                                           : f32x4{0.f, 0.f, 0.f, 0.f};
-        };
-        if (q0 < units) load_u();
-        // The weights are needed only by the MFMAs: issued after the merge's
-        // loads, they stream while the merge is folded.
-        load_weights<NJ>(wf, a, h, dp);
-        if (t < ntok) {
-            float m = -FLT_MAX;
-#pragma unroll
-            for (int j = 0; j < BATCH; ++j) m = fmaxf(m, msv[j]);
-            float l = 0.f;
-#pragma unroll
-            for (int j = 0; j < BATCH; ++j) {
-                const float w = merge_weight(msv[j], m);
-                wts[t][j] = w;
-                if (j < a.nsplit) l = __builtin_fmaf(w, lsv[j], l);
-            }
-            lsum[t] = l;
-            if (dp == 0) {
-                const int64_t orow = (int64_t)(t0 + t) * a.H + h;
-                a.out_max[orow] = m;
-                a.out_sum[orow] = l;
-            }
-        }
-        lds_barrier();
-        for (; q0 < units; q0 += NU * kThreads) {
-            if (q0 != (int)threadIdx.x) load_u();
-#pragma unroll
-            for (int r = 0; r < NU; ++r) {
-                const int tt = min((q0 + r * kThreads) >> 7, TB - 1);
-                f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                for (int j = 0; j < BATCH; ++j)
-                    if (j < a.nsplit) merge_add_cols(wts[tt][j], u[r][j], acc);
-                put(q0, r, merge_finish(acc, lsum[tt]));
-            }
-        }
-    } else {
-        load_weights<NJ>(wf, a, h, dp);
-        for (int q0 = threadIdx.x; q0 < units; q0 += NU * kThreads) {
-            int64_t base[NU];
-            int col[NU];
-            unit_rows(q0, base, col);
-            f32x4 acc[NU];
-            float m[NU], l[NU];
-            merge_units<NU, BATCH>(a.part_o, a.part_m, a.part_l, base, col, a.H, a.nsplit, acc, m, l);
-#pragma unroll
-            for (int r = 0; r < NU; ++r) {
-                put(q0, r, merge_finish(acc[r], l[r]));
-                const int q = q0 + r * kThreads;
-                if (q < units && (q & 127) == 0 && dp == 0) {
-                    const int64_t orow = (int64_t)(t0 + (q >> 7)) * a.H + h;
-                    a.out_max[orow] = m[r];
-                    a.out_sum[orow] = l[r];
-                }
+        for (int r = 0; r < NU; ++r) {
+            put(q0, r, merge_finish(acc[r], l[r]));
+            const int q = q0 + r * kThreads;
+            if (q < units && (q & 127) == 0 && dp == 0) {
+                const int64_t orow = (int64_t)(t0 + (q >> 7)) * a.H + h;
+                a.out_max[orow] = m[r];
+                a.out_sum[orow] = l[r];
             }
         }
     }
