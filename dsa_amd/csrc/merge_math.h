@@ -96,6 +96,53 @@ __device__ __forceinline__ void merge_units(const float* __restrict__ part_o, co
     }
 }
 
+// merge_units for NU column groups of ONE row: the row's max, weights and sum
+// are computed once and applied to every group -- per value the operations
+// of merge_units, so the same bits, with 1 / NU of its m / l loads and
+// exponentials.
+template <int NU, int BATCH = kMergeBatch>
+__device__ __forceinline__ void merge_row(const float* __restrict__ part_o, const float* __restrict__ part_m,
+                                          const float* __restrict__ part_l, int64_t base, const int (&col)[NU],
+                                          int H, int nsplit, merge_f32x4 (&acc)[NU], float& m, float& l) {
+    m = -FLT_MAX;
+    l = 0.f;
+#pragma unroll
+    for (int r = 0; r < NU; ++r) acc[r] = merge_f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int s0 = 0; s0 < nsplit; s0 += BATCH) {
+        merge_f32x4 u[NU][BATCH];
+        float ms[BATCH], ls[BATCH];
+#pragma unroll
+        for (int j = 0; j < BATCH; ++j) {
+            const bool live = s0 + j < nsplit;
+            const int64_t row = base + (int64_t)(live ? s0 + j : 0) * H;
+            ms[j] = live ? part_m[row] : -FLT_MAX;
+            ls[j] = live ? part_l[row] : 0.f;
+#pragma unroll
+            for (int r = 0; r < NU; ++r)
+                u[r][j] = live ? *reinterpret_cast<const merge_f32x4*>(part_o + row * 512 + col[r])
+                               : merge_f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+        float mb = m;
+#pragma unroll
+        for (int j = 0; j < BATCH; ++j) mb = fmaxf(mb, ms[j]);
+        if (s0 > 0) {
+            const float alpha = merge_weight(m, mb);
+            l *= alpha;
+#pragma unroll
+            for (int r = 0; r < NU; ++r) acc[r] *= alpha;
+        }
+        m = mb;
+#pragma unroll
+        for (int j = 0; j < BATCH; ++j)
+            if (s0 + j < nsplit) {
+                const float w = merge_weight(ms[j], m);
+                l = __builtin_fmaf(w, ls[j], l);
+#pragma unroll
+                for (int r = 0; r < NU; ++r) merge_add_cols(w, u[r][j], acc[r]);
+            }
+    }
+}
+
 __device__ __forceinline__ merge_bf16x4 merge_finish(merge_f32x4 acc, float l) {
     merge_bf16x4 o;
     o[0] = (__bf16)(acc[0] / l);

@@ -280,10 +280,10 @@ __global__ __launch_bounds__(kThreads) void project_kernel(UvArgs a) {
 template <int NJ, int BATCH>
 __global__ __launch_bounds__(kThreads) void merge_uv_kernel(UvArgs a) {
     constexpr int TB = 16;
-    // Units of 4 columns per thread per pass: the split loads of a pass in
-    // registers stay near 128 VGPRs (64 with the second weight tile; 96 for
-    // BATCH 4, whose weights-per-unit bookkeeping would spill at 128).
-    constexpr int BUDGET = NJ == 2 ? 16 : BATCH == 4 ? 24 : 32;
+    // Units of 4 columns per thread per pass (a power of two dividing 128):
+    // the split loads of a pass in registers stay near 128 VGPRs (64 with
+    // the second weight tile).
+    constexpr int BUDGET = NJ == 2 ? 16 : 32;
     constexpr int NU = BUDGET / BATCH < 1 ? 1 : BUDGET / BATCH < 8 ? BUDGET / BATCH : 8;
     __shared__ __attribute__((aligned(16))) uint8_t tile[TB * 1024];
     int h, blk, dp;
@@ -293,42 +293,32 @@ __global__ __launch_bounds__(kThreads) void merge_uv_kernel(UvArgs a) {
 
     bf16x8 wf[NJ][kKSteps];
 
-    // Units of 4 columns: 128 per token row.  Rows past ntok are left
-    // unwritten: they feed only the D columns of tokens that are never
-    // stored (an MFMA's column n reads column n of B only).
-    const int units = ntok * 128;
-    auto unit_rows = [&](int q0, int64_t (&base)[NU], int (&col)[NU]) {
-#pragma unroll
-        for (int r = 0; r < NU; ++r) {
-            const int q = q0 + r * kThreads;
-            base[r] = (int64_t)(q < units ? t0 + (q >> 7) : t0) * a.nsplit * a.H + h;
-            col[r] = (q & 127) * 4;
-        }
-    };
-    auto put = [&](int q0, int r, merge_bf16x4 o) {
-        const int q = q0 + r * kThreads, c = q & 127;
-        if (q < units) *reinterpret_cast<merge_bf16x4*>(tile + tile_off(q >> 7, c >> 1) + ((c & 1) << 3)) = o;
-    };
-    // Every thread folds its own units' max, weights and sum (the same for the
-    // 128 units of a row): a per-row fold into LDS behind one thread measured
-    // slower, its barrier sitting in the merge's critical path.
+    // A thread merges NU units of 4 columns of one token row (its row's max,
+    // weights and sum computed once): G = 128 / NU threads per row, 2 NU rows
+    // per pass, unit r of thread c of a row at columns 4 (c + G r); each half
+    // of a wave (G = 32) reads 512 contiguous bytes per load.  Rows past ntok
+    // are left unwritten: they feed only the D columns of tokens that are
+    // never stored (an MFMA's column n reads column n of B only).
+    constexpr int G = 128 / NU;
+    const int rsub = threadIdx.x / G, cg = threadIdx.x % G;
     load_weights<NJ>(wf, a, h, dp);
-    for (int q0 = threadIdx.x; q0 < units; q0 += NU * kThreads) {
-        int64_t base[NU];
+    for (int tt = rsub; tt < ntok; tt += kThreads / G) {
+        const int64_t base = (int64_t)(t0 + tt) * a.nsplit * a.H + h;
         int col[NU];
-        unit_rows(q0, base, col);
+#pragma unroll
+        for (int r = 0; r < NU; ++r) col[r] = 4 * (cg + G * r);
         f32x4 acc[NU];
-        float m[NU], l[NU];
-        merge_units<NU, BATCH>(a.part_o, a.part_m, a.part_l, base, col, a.H, a.nsplit, acc, m, l);
+        float m, l;
+        merge_row<NU, BATCH>(a.part_o, a.part_m, a.part_l, base, col, a.H, a.nsplit, acc, m, l);
 #pragma unroll
         for (int r = 0; r < NU; ++r) {
-            put(q0, r, merge_finish(acc[r], l[r]));
-            const int q = q0 + r * kThreads;
-            if (q < units && (q & 127) == 0 && dp == 0) {
-                const int64_t orow = (int64_t)(t0 + (q >> 7)) * a.H + h;
-                a.out_max[orow] = m[r];
-                a.out_sum[orow] = l[r];
-            }
+            const int c = cg + G * r;
+            *reinterpret_cast<merge_bf16x4*>(tile + tile_off(tt, c >> 1) + ((c & 1) << 3)) = merge_finish(acc[r], l);
+        }
+        if (cg == 0 && dp == 0) {
+            const int64_t orow = (int64_t)(t0 + tt) * a.H + h;
+            a.out_max[orow] = m;
+            a.out_sum[orow] = l;
         }
     }
     lds_barrier();
