@@ -29,19 +29,20 @@
 // element the chain is the same 16 MFMAs in the same order in both kernels,
 // which is what makes merge_uv's result equal project_uv(merge) bit for bit.
 //
-// * project_kernel<TB, NJ>: workgroup = (head, chunk of tokens, d part).  The
-//   weights are loaded once; the chunk is walked in tiles of TB tokens
-//   through two LDS buffers: tile i+1's latent rows are loaded into
-//   registers while tile i is multiplied, then written to the other buffer
-//   (one barrier per tile).  Every latent byte is read from HBM once.  The
-//   B fragments are read from LDS in groups of 8, one group ahead of the
+// * project_kernel<NJ>: workgroup = (head, chunk of tokens, d part).  The
+//   weights are loaded once; the chunk is walked in tiles of 32 tokens
+//   through four LDS buffers, the latent rows loaded straight into LDS
+//   (buffer_load ... lds), three tiles in flight while one is multiplied,
+//   one LDS-only barrier per tile.  Every latent byte is read from HBM once.
+//   The B fragments are read from LDS in groups of 8, one group ahead of the
 //   MFMAs that use them.
 // * merge_uv_kernel<NJ, BATCH>: workgroup = (head, 16 tokens, d part).  The
-//   merge fills the tile with 32 / BATCH (16 / BATCH with two weight tiles;
-//   1 to 8) units of 4 columns per thread per pass, every split load of a
-//   pass in flight at once, the batch width matched to the split count.
+//   merge fills the tile: each thread merges 32 / BATCH (16 / BATCH with two
+//   weight tiles; 1 to 8) units of 4 columns of one token row, the row's
+//   max, weights and sum once per thread, every split load in flight at
+//   once, the batch width matched to the split count.
 //
-// LDS tile: TB latent rows of 1 KiB; 16-byte chunk c of row t sits at chunk
+// LDS tile: latent rows of 1 KiB; 16-byte chunk c of row t sits at chunk
 // c ^ (t & 15), so the 16 rows one B-operand read touches hit distinct banks.
 #include <hip/hip_runtime.h>
 #include <float.h>
