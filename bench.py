@@ -74,6 +74,8 @@ def algorithmic_units(shape, fp8=False):
 class Call:
     """One preallocated forward call through the C ABI."""
 
+    _uv_sets = 0  # W_UV weight tensors made so far (each call's own seed)
+
     def __init__(self, data, config: Tuning, block_table=None, fp8=False, uv_dim=0):
         self.data = data
         q = data[0]
@@ -116,7 +118,8 @@ class Call:
         # (one layer's [H, dv, 512]), so rotating calls do not share them.
         self.uv = uv_dim
         if uv_dim:
-            gen = torch.Generator(device=dev).manual_seed(uv_dim + len(self.args))
+            Call._uv_sets += 1
+            gen = torch.Generator(device=dev).manual_seed(1000 * uv_dim + Call._uv_sets)
             self.w = (torch.randn((h, uv_dim, 512), generator=gen, device=dev) / 512 ** 0.5).bfloat16()
             self.out_v = torch.empty((b, sq, h, uv_dim), device=dev, dtype=torch.bfloat16)
             self.uv_args = (p(self.w), uv_dim * 512, p(self.out_v))
