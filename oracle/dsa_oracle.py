@@ -205,7 +205,10 @@ def project_uv_ref(output, w_uv):
     [..., H, 512]``, ``w_uv [H, dv, 512]``; returns float64 ``[..., H, dv]``."""
     x = output.detach().cpu().double()
     w = w_uv.detach().cpu().double()
-    return (x.unsqueeze(-2) * w).sum(-1)
+    heads = x.shape[-2]
+    xs = x.reshape(-1, heads, x.shape[-1]).transpose(0, 1)   # [H, T, 512]
+    out = torch.bmm(xs, w.transpose(1, 2))                    # [H, T, dv], FP64 on the CPU
+    return out.transpose(0, 1).reshape(*x.shape[:-1], w.shape[1])
 
 
 def float_key(values):
