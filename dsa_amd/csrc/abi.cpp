@@ -199,7 +199,8 @@ int dsa_partial_elems(const dsa_plan* plan, int B, int SQ, int H, int64_t* part_
 }
 
 int dsa_merge(const float* part_o, const float* part_m, const float* part_l, uint16_t* out, float* out_max,
-              float* out_sum, int tokens, int H, int split, hipStream_t stream) {
+              float* out_sum, int tokens, int H, int split, void* stream_) {
+    const hipStream_t stream = static_cast<hipStream_t>(stream_);
     if (!part_o || !part_m || !part_l || !out || !out_max || !out_sum) return fail(-1, "NULL pointer argument");
     if (tokens <= 0 || H <= 0 || split <= 0)
         return fail(-1, "tokens, H, split must be positive (got %d, %d, %d)", tokens, H, split);
@@ -236,7 +237,8 @@ int check_uv(const uint16_t* w_uv, int64_t w_head_stride, const uint16_t* out_v,
 extern "C" {
 
 int dsa_project_uv(const uint16_t* output, const uint16_t* w_uv, int64_t w_head_stride, uint16_t* out_v,
-                   int tokens, int H, int dv, hipStream_t stream) {
+                   int tokens, int H, int dv, void* stream_) {
+    const hipStream_t stream = static_cast<hipStream_t>(stream_);
     if (!output) return fail(-1, "NULL pointer argument");
     if (int rc = check_uv(w_uv, w_head_stride, out_v, tokens, H, dv)) return rc;
     if ((uintptr_t)output & 15) return fail(-1, "output must be 16-byte aligned");
@@ -248,7 +250,8 @@ int dsa_project_uv(const uint16_t* output, const uint16_t* w_uv, int64_t w_head_
 
 int dsa_merge_uv(const float* part_o, const float* part_m, const float* part_l, const uint16_t* w_uv,
                  int64_t w_head_stride, uint16_t* out_v, float* out_max, float* out_sum, int tokens, int H,
-                 int split, int dv, hipStream_t stream) {
+                 int split, int dv, void* stream_) {
+    const hipStream_t stream = static_cast<hipStream_t>(stream_);
     if (!part_o || !part_m || !part_l || !out_max || !out_sum) return fail(-1, "NULL pointer argument");
     if (int rc = check_uv(w_uv, w_head_stride, out_v, tokens, H, dv)) return rc;
     if (split <= 0) return fail(-1, "split must be positive (got %d)", split);
@@ -378,7 +381,8 @@ extern "C" {
 
 int dsa_fwd(const uint16_t* q, const uint16_t* kv, const uint16_t* q_rope, const uint16_t* k_rope,
             const int32_t* idx, uint16_t* out, float* out_max, float* out_sum, float* part_o, float* part_m,
-            float* part_l, int B, int SQ, int H, int L, int TOPK, const dsa_plan* plan, hipStream_t stream) {
+            float* part_l, int B, int SQ, int H, int L, int TOPK, const dsa_plan* plan, void* stream_) {
+    const hipStream_t stream = static_cast<hipStream_t>(stream_);
     return fwd_impl(q, kv, q_rope, k_rope, idx, out, out_max, out_sum, part_o, part_m, part_l, B, SQ, H, L,
                     TOPK, nullptr, plan, stream, true);
 }
@@ -386,7 +390,8 @@ int dsa_fwd(const uint16_t* q, const uint16_t* kv, const uint16_t* q_rope, const
 int dsa_fwd_main(const uint16_t* q, const uint16_t* kv, const uint16_t* q_rope, const uint16_t* k_rope,
                  const int32_t* idx, uint16_t* out, float* out_max, float* out_sum, float* part_o,
                  float* part_m, float* part_l, int B, int SQ, int H, int L, int TOPK, const dsa_plan* plan,
-                 hipStream_t stream) {
+                 void* stream_) {
+    const hipStream_t stream = static_cast<hipStream_t>(stream_);
     return fwd_impl(q, kv, q_rope, k_rope, idx, out, out_max, out_sum, part_o, part_m, part_l, B, SQ, H, L,
                     TOPK, nullptr, plan, stream, false);
 }
@@ -394,7 +399,8 @@ int dsa_fwd_main(const uint16_t* q, const uint16_t* kv, const uint16_t* q_rope, 
 int dsa_fwd_opts(const uint16_t* q, const uint16_t* kv, const uint16_t* q_rope, const uint16_t* k_rope,
                  const int32_t* idx, uint16_t* out, float* out_max, float* out_sum, float* part_o, float* part_m,
                  float* part_l, int B, int SQ, int H, int L, int TOPK, const dsa_fwd_options* opts,
-                 const dsa_plan* plan, hipStream_t stream) {
+                 const dsa_plan* plan, void* stream_) {
+    const hipStream_t stream = static_cast<hipStream_t>(stream_);
     return fwd_impl(q, kv, q_rope, k_rope, idx, out, out_max, out_sum, part_o, part_m, part_l, B, SQ, H, L,
                     TOPK, opts, plan, stream, true);
 }
@@ -402,7 +408,8 @@ int dsa_fwd_opts(const uint16_t* q, const uint16_t* kv, const uint16_t* q_rope, 
 int dsa_fwd_main_opts(const uint16_t* q, const uint16_t* kv, const uint16_t* q_rope, const uint16_t* k_rope,
                       const int32_t* idx, uint16_t* out, float* out_max, float* out_sum, float* part_o,
                       float* part_m, float* part_l, int B, int SQ, int H, int L, int TOPK,
-                      const dsa_fwd_options* opts, const dsa_plan* plan, hipStream_t stream) {
+                      const dsa_fwd_options* opts, const dsa_plan* plan, void* stream_) {
+    const hipStream_t stream = static_cast<hipStream_t>(stream_);
     return fwd_impl(q, kv, q_rope, k_rope, idx, out, out_max, out_sum, part_o, part_m, part_l, B, SQ, H, L,
                     TOPK, opts, plan, stream, false);
 }
@@ -412,7 +419,8 @@ int dsa_fwd_main_opts(const uint16_t* q, const uint16_t* kv, const uint16_t* q_r
 extern "C" {
 
 int dsa_indexer_logits(const uint16_t* q_idx, const uint16_t* k_idx, const float* weights, const int32_t* lengths,
-                       float* logits, int B, int SQ, int HI, int L, hipStream_t stream) {
+                       float* logits, int B, int SQ, int HI, int L, void* stream_) {
+    const hipStream_t stream = static_cast<hipStream_t>(stream_);
     if (!q_idx || !k_idx || !weights || !lengths || !logits) return fail(-1, "NULL pointer argument");
     if (B <= 0 || SQ <= 0 || L <= 0) return fail(-1, "B, SQ, L must be positive (got %d, %d, %d)", B, SQ, L);
     if (HI != 32 && HI != 64) return fail(-1, "indexer heads must be 32 or 64 (got %d)", HI);
@@ -453,7 +461,8 @@ int dsa_indexer_logits(const uint16_t* q_idx, const uint16_t* k_idx, const float
 }
 
 int dsa_indexer_topk(const float* logits, const int32_t* lengths, int32_t* indices, int B, int SQ, int L, int TOPK,
-                     hipStream_t stream) {
+                     void* stream_) {
+    const hipStream_t stream = static_cast<hipStream_t>(stream_);
     if (!logits || !lengths || !indices) return fail(-1, "NULL pointer argument");
     if (B <= 0 || SQ <= 0 || L <= 0 || TOPK <= 0)
         return fail(-1, "B, SQ, L, TOPK must be positive (got %d, %d, %d, %d)", B, SQ, L, TOPK);
@@ -473,7 +482,8 @@ int64_t dsa_indexer_topk_ws_bytes(int B, int SQ, int L, int TOPK) {
 }
 
 int dsa_indexer_topk_ws(const float* logits, const int32_t* lengths, int32_t* indices, int B, int SQ, int L,
-                        int TOPK, void* workspace, int64_t workspace_bytes, hipStream_t stream) {
+                        int TOPK, void* workspace, int64_t workspace_bytes, void* stream_) {
+    const hipStream_t stream = static_cast<hipStream_t>(stream_);
     const int64_t need = dsa_indexer_topk_ws_bytes(B, SQ, L, TOPK);
     if (!workspace || need == 0) return dsa_indexer_topk(logits, lengths, indices, B, SQ, L, TOPK, stream);
     if (!logits || !lengths || !indices) return fail(-1, "NULL pointer argument");

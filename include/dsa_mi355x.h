@@ -18,8 +18,9 @@
  *     bit patterns; all tensors dense row-major (contiguous);
  *   - the library allocates and frees nothing, and keeps no state across calls
  *     other than read-only kernel handles;
- *   - work is enqueued on `stream` (NULL = the default stream); no call
- *     synchronises the device;
+ *   - work is enqueued on `stream`, a hipStream_t passed as void* (NULL = the
+ *     default stream); no call synchronises the device.  The header needs no
+ *     HIP header, so C and FFI callers include it on its own;
  *   - return value: 0 = success, < 0 = invalid argument (nothing was enqueued),
  *     > 0 = a hipError_t from the launch; dsa_last_error() then describes it.
  *     No entry point throws.
@@ -34,7 +35,6 @@
 #define DSA_MI355X_H
 
 #include <stdint.h>
-#include <hip/hip_runtime_api.h>
 
 #ifdef __cplusplus
 extern "C" {
@@ -123,7 +123,7 @@ int dsa_fwd(const uint16_t* q, const uint16_t* kv, const uint16_t* q_rope,
             uint16_t* out, float* out_max, float* out_sum,
             float* part_o, float* part_m, float* part_l,
             int B, int SQ, int H, int L, int TOPK,
-            const dsa_plan* plan, hipStream_t stream);
+            const dsa_plan* plan, void* stream);
 
 /*
  * The main kernel of dsa_fwd alone (dsa/api.py:115-123): with plan->split == 1
@@ -137,7 +137,7 @@ int dsa_fwd_main(const uint16_t* q, const uint16_t* kv, const uint16_t* q_rope,
                  uint16_t* out, float* out_max, float* out_sum,
                  float* part_o, float* part_m, float* part_l,
                  int B, int SQ, int H, int L, int TOPK,
-                 const dsa_plan* plan, hipStream_t stream);
+                 const dsa_plan* plan, void* stream);
 
 /*
  * Options beyond the reference's operator contract, which fixes the scale at
@@ -200,7 +200,7 @@ int dsa_fwd_opts(const uint16_t* q, const uint16_t* kv, const uint16_t* q_rope,
                  uint16_t* out, float* out_max, float* out_sum,
                  float* part_o, float* part_m, float* part_l,
                  int B, int SQ, int H, int L, int TOPK,
-                 const dsa_fwd_options* opts, const dsa_plan* plan, hipStream_t stream);
+                 const dsa_fwd_options* opts, const dsa_plan* plan, void* stream);
 
 /*
  * dsa_plan_for for a call with options: with kv_format DSA_KV_FP8 it plans
@@ -215,7 +215,7 @@ int dsa_fwd_main_opts(const uint16_t* q, const uint16_t* kv, const uint16_t* q_r
                       uint16_t* out, float* out_max, float* out_sum,
                       float* part_o, float* part_m, float* part_l,
                       int B, int SQ, int H, int L, int TOPK,
-                      const dsa_fwd_options* opts, const dsa_plan* plan, hipStream_t stream);
+                      const dsa_fwd_options* opts, const dsa_plan* plan, void* stream);
 
 /*
  * FP32 merge of split partials (dsa/merge.py:13-91):
@@ -226,7 +226,7 @@ int dsa_fwd_main_opts(const uint16_t* q, const uint16_t* kv, const uint16_t* q_r
  */
 int dsa_merge(const float* part_o, const float* part_m, const float* part_l,
               uint16_t* out, float* out_max, float* out_sum,
-              int tokens, int H, int split, hipStream_t stream);
+              int tokens, int H, int split, void* stream);
 
 /*
  * W_UV output projection: the step after the attention (no reference
@@ -248,7 +248,7 @@ int dsa_merge(const float* part_o, const float* part_m, const float* part_l,
  * FP32 accumulation, one bf16 rounding.
  */
 int dsa_project_uv(const uint16_t* output, const uint16_t* w_uv, int64_t w_head_stride,
-                   uint16_t* out_v, int tokens, int H, int dv, hipStream_t stream);
+                   uint16_t* out_v, int tokens, int H, int dv, void* stream);
 
 /*
  * dsa_merge and dsa_project_uv in one launch (no reference counterpart):
@@ -260,7 +260,7 @@ int dsa_project_uv(const uint16_t* output, const uint16_t* w_uv, int64_t w_head_
 int dsa_merge_uv(const float* part_o, const float* part_m, const float* part_l,
                  const uint16_t* w_uv, int64_t w_head_stride, uint16_t* out_v,
                  float* out_max, float* out_sum, int tokens, int H, int split, int dv,
-                 hipStream_t stream);
+                 void* stream);
 
 /*
  * Lightning indexer: the token selector that produces `idx` for dsa_fwd (the
@@ -281,10 +281,10 @@ int dsa_merge_uv(const float* part_o, const float* part_m, const float* part_l,
  */
 int dsa_indexer_logits(const uint16_t* q_idx, const uint16_t* k_idx, const float* weights,
                        const int32_t* lengths, float* logits,
-                       int B, int SQ, int HI, int L, hipStream_t stream);
+                       int B, int SQ, int HI, int L, void* stream);
 
 int dsa_indexer_topk(const float* logits, const int32_t* lengths, int32_t* indices,
-                     int B, int SQ, int L, int TOPK, hipStream_t stream);
+                     int B, int SQ, int L, int TOPK, void* stream);
 
 /*
  * dsa_indexer_topk with a workspace (no reference counterpart, like the
@@ -298,7 +298,7 @@ int64_t dsa_indexer_topk_ws_bytes(int B, int SQ, int L, int TOPK);
 
 int dsa_indexer_topk_ws(const float* logits, const int32_t* lengths, int32_t* indices,
                         int B, int SQ, int L, int TOPK, void* workspace, int64_t workspace_bytes,
-                        hipStream_t stream);
+                        void* stream);
 
 #ifdef __cplusplus
 }

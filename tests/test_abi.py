@@ -248,3 +248,44 @@ def test_w_uv_entry_points_validate_before_any_launch():
     assert lib.dsa_merge_uv(fake, fake, fake, fake, stride, fake, fake, fake, 8, 16, 2, 96, None) < 0
     assert lib.dsa_merge_uv(ctypes.c_void_p((1 << 20) + 4), fake, fake, fake, stride, fake, fake, fake,
                             8, 16, 2, 128, None) < 0
+
+
+C_PROGRAM = r"""
+#include <stdio.h>
+#include "dsa_mi355x.h"
+int main(void) {
+    dsa_plan plan;
+    int64_t po = 0, pml = 0;
+    int rc = dsa_plan_for(8, 1, 128, 32768, 2048, 256, &plan);
+    if (rc == 0) rc = dsa_partial_elems(&plan, 8, 1, 128, &po, &pml);
+    int bad = dsa_fwd(0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 8, 1, 128, 32768, 2048, &plan, 0);
+    printf("%d %d %d %lld %lld %d %s\n", dsa_version(), rc, plan.split, (long long)po, (long long)pml, bad,
+           dsa_last_error());
+    return 0;
+}
+"""
+
+
+def test_header_is_plain_c_and_links(tmp_path):
+    """A C99 program includes the header on its own (no HIP headers, no
+    platform macro) and calls the library: what a cgo / FFI binding does."""
+    import shutil
+    import subprocess
+    gcc = shutil.which("gcc")
+    if gcc is None:
+        pytest.skip("gcc not available")
+    lib = _lib.load()._name
+    src = tmp_path / "t.c"
+    src.write_text(C_PROGRAM)
+    exe = tmp_path / "t"
+    libdir = str(Path(lib).parent)
+    res = subprocess.run([gcc, "-std=c99", "-Wall", "-Wextra", "-Werror", f"-I{HEADER.parent}", str(src),
+                          f"-L{libdir}", "-ldsa_mi355x", f"-Wl,-rpath,{libdir}", "-o", str(exe)],
+                         capture_output=True, text=True)
+    assert res.returncode == 0, res.stderr
+    out = subprocess.run([str(exe)], capture_output=True, text=True, timeout=60)
+    assert out.returncode == 0, out.stderr
+    version, rc, split, po, pml, bad, *msg = out.stdout.split()
+    assert int(version) == _lib.load().dsa_version() and int(rc) == 0 and int(split) >= 1
+    assert (int(po) > 0) == (int(split) > 1) and int(pml) * 512 == int(po)
+    assert int(bad) < 0 and "NULL" in " ".join(msg)
