@@ -175,8 +175,9 @@ def test_forward_w_uv_with_scale_paged_and_fp8():
     rows = dsa_amd.quantize_kv_fp8(kv, kr)
     for kw in ({"scale": 192 ** -0.5}, {"kv": rows, "k_rope": None}):
         args = {"kv": kv, "k_rope": kr, **kw}
-        out_v, mx, sm = dsa_amd.forward(q, args["kv"], qr, args["k_rope"], ids, w_uv=w,
-                                        scale=kw.get("scale"))
+        (out_v, mx, sm), launches = dsa_amd.forward(q, args["kv"], qr, args["k_rope"], ids, w_uv=w,
+                                                    scale=kw.get("scale"), return_kernels=True)
+        assert launches[-1].name == "merge_uv", launches  # the planner splits this shape
         out, mx2, sm2 = dsa_amd.forward(q, args["kv"], qr, args["k_rope"], ids, scale=kw.get("scale"))
         torch.cuda.synchronize()
         assert torch.equal(out_v, dsa_amd.project_uv(out, w)), sorted(kw)
