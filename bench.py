@@ -21,9 +21,20 @@ batch.  ``ms_per_step`` is the host wall clock of the K timed calls.
 ``breakdown.eager_call_us`` is the median wall clock of one ``dsa_amd.forward``
 call (checks, allocation, launches) followed by a device synchronisation.
 
+The metric is "decode B=8 + prefill": the default line is C2 (``value``)
+and carries a ``prefill`` object with the C5 and C4 lines' span, roofline
+(MFMA-bound), breakdown and CPU baseline, timed the same way (``--no-prefill``
+leaves it out).  ``roofline.frac`` is the main kernel's (its average launch);
+``roofline.frac_span`` is the whole call's, split merge included.
+
+The warm-up and every timed batch walk one continuous rotation over the input
+sets, so the warm-up leaves none of the first timed sets in the caches.
+
 cpu_baseline: the CPU oracle (oracle/dsa_oracle.py, a restatement of the
 reference's FP32 PyTorch gather+softmax path) timed on this host on a bounded
-sample of the same workload.
+sample of the same workload, with every CPU the process may use (capped by
+OMP_NUM_THREADS when the host sets it); the line records the counts and the
+CPU model.
 """
 from __future__ import annotations
 
@@ -32,6 +43,7 @@ import ctypes
 import json
 import os
 import statistics
+import subprocess
 import sys
 import time
 from pathlib import Path
@@ -158,7 +170,21 @@ class Call:
             _lib.check(rc, "dsa_merge")
 
 
-def _batch_us(calls, steps, stream_obj, work):
+class Rotation:
+    """Input sets taken in one continuous cyclic order across the warm-up and
+    every timed batch, so a set comes round again only after all the others
+    (len(calls) - 1 calls later), whatever K and W are."""
+
+    def __init__(self, calls):
+        self.calls, self.next = calls, 0
+
+    def take(self):
+        call = self.calls[self.next % len(self.calls)]
+        self.next += 1
+        return call
+
+
+def _batch_us(rot, steps, stream_obj, work):
     """Device time per call of ``steps`` back-to-back launches between two
     HIP events on the launch stream (no event inside the batch, so the
     per-event cost of a few microseconds is not charged to every call)."""
@@ -166,8 +192,8 @@ def _batch_us(calls, steps, stream_obj, work):
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     e0.record(stream_obj)
-    for i in range(steps):
-        work(calls[i % len(calls)], stream)
+    for _ in range(steps):
+        work(rot.take(), stream)
     e1.record(stream_obj)
     torch.cuda.synchronize()
     return e0.elapsed_time(e1) * 1e3 / steps
@@ -179,23 +205,36 @@ def time_calls(calls, steps, warmup):
     on both sides: returns (host wall seconds of those K calls, span µs per
     call).  Then K main-kernel launches alone and K merges alone, timed the
     same way: (main µs, merge µs) per launch, the main kernel's average
-    duration being the roofline's denominator."""
+    duration being the roofline's denominator.  All of it walks one
+    continuous rotation over the input sets (``Rotation``): the warm-up does
+    not leave the first timed sets in the cache."""
     stream_obj = torch.cuda.current_stream()
     stream = ctypes.c_void_p(stream_obj.cuda_stream)
+    rot = Rotation(calls)
     both = lambda c, s: (c.main(s), c.merge(s))  # noqa: E731
-    for i in range(warmup):
-        both(calls[i % len(calls)], stream)
+    for _ in range(warmup):
+        both(rot.take(), stream)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    span = _batch_us(calls, steps, stream_obj, both)
+    span = _batch_us(rot, steps, stream_obj, both)
     wall = time.perf_counter() - t0
-    main = _batch_us(calls, steps, stream_obj, lambda c, s: c.main(s))
-    merge = _batch_us(calls, steps, stream_obj, lambda c, s: c.merge(s))
+    main = _batch_us(rot, steps, stream_obj, lambda c, s: c.main(s))
+    merge = _batch_us(rot, steps, stream_obj, lambda c, s: c.merge(s))
     return wall, main, merge, span
 
 
 def cpu_model():
-    """The host CPU's model name (/proc/cpuinfo), for the baseline record."""
+    """The host CPU's model name, for the baseline record: ``lscpu``'s "Model
+    name" (with its vendor), else /proc/cpuinfo's "model name"."""
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        fields = dict(ln.split(":", 1) for ln in out.splitlines() if ":" in ln)
+        name = fields.get("Model name", "").strip()
+        vendor = fields.get("Vendor ID", "").strip()
+        if name:
+            return f"{name} ({vendor})" if vendor and vendor not in name else name
+    except (OSError, subprocess.SubprocessError, ValueError):
+        pass
     try:
         for ln in Path("/proc/cpuinfo").read_text().splitlines():
             if ln.startswith("model name"):
@@ -203,6 +242,21 @@ def cpu_model():
     except OSError:
         pass
     return None
+
+
+# Thread and CPU counts of the CPU baseline, filled in by main().
+CPU_COUNTS = {}
+
+
+def cpu_threads():
+    """Threads for the CPU baseline: every CPU this process may run on
+    (``os.sched_getaffinity``), capped by OMP_NUM_THREADS when the host sets
+    it (the GPU box gives each GPU a 16-CPU share and says so there), and the
+    counts it was derived from."""
+    avail = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    omp = os.environ.get("OMP_NUM_THREADS", "")
+    threads = min(avail, int(omp)) if omp.isdigit() and int(omp) > 0 else avail
+    return threads, {"os_cpu_count": os.cpu_count(), "affinity_cpus": avail, "OMP_NUM_THREADS": omp or None}
 
 
 def eager_us(data, config, samples=30):
@@ -252,19 +306,22 @@ def cpu_baseline(name, data, budget_s=10.0):
             break
     per_call_us = statistics.median(times) * 1e6 * len(tokens) / len(sample)
     return {"value": round(per_call_us, 1), "unit": "µs/call", "cores": torch.get_num_threads(),
-            "kind": "port", "cpu": cpu_model(),
+            "kind": "port", "cpu": cpu_model(), **CPU_COUNTS,
             "sample": (f"FP32 torch gather+softmax oracle on {len(sample)} of {len(tokens)} tokens of one "
-                       f"{name} call, median of {len(times)} runs, scaled to a full call"
+                       f"{name} call, median of {len(times)} runs after one warm-up, scaled to a full call; "
+                       f"inputs already on the host (generation and copies not timed)"
                        + ("; kv dequantized from the fp8 rows beforehand (not timed)" if fp8 else ""))}
 
 
 def traffic_from_profiles(name):
-    """HBM bytes per main-kernel launch measured by rocprofv3 --pmc, if a
-    summary for this workload is committed under profiles/."""
+    """(HBM bytes per main-kernel launch measured by rocprofv3 --pmc, the
+    commit the profiled build came from), if a summary for this workload is
+    committed under profiles/."""
     path = ROOT / "profiles" / f"sparse_mla_fwd_{name}_hbm_traffic.json"
     if not path.exists():
-        return None
-    return json.loads(path.read_text()).get("hbm_bytes_per_launch")
+        return None, None
+    rec = json.loads(path.read_text())
+    return rec.get("hbm_bytes_per_launch"), rec.get("commit")
 
 
 def paged(data, block_size, seed):
@@ -284,11 +341,13 @@ def paged(data, block_size, seed):
     return (q, kv_pool, qr, kr_pool, ids), perm.view(batch, per).int().contiguous()
 
 
-def run(name, args):
+def run(name, args, overrides=True):
+    """One workload's line.  ``overrides=False`` ignores --plan and --rotate
+    (the prefill leg that follows a decode line uses its own defaults)."""
     shape = BASELINE_CONFIGS[name]
-    rotate = args.rotate if args.rotate else DEFAULT_ROTATE[name]
+    rotate = args.rotate if args.rotate and overrides else DEFAULT_ROTATE[name]
     config = dsa_amd.select(shape, kv_fp8=args.fp8)
-    if args.plan:
+    if args.plan and overrides:
         v = [int(x) for x in args.plan.split(",")]
         bm, split, kv_waves, mfma = v[:4]
         bn, stages = (v[4], v[5]) if len(v) > 4 else (64, 2)
@@ -315,8 +374,11 @@ def run(name, args):
     bound = BOUND[name]
     if bound == "hbm":
         achieved, peak, unit = gbytes / (main_us * 1e-6) / 1e9, HBM_PEAK_GBS, "GB/s"
+        achieved_span = gbytes / (span_us * 1e-6) / 1e9
     else:
         achieved, peak, unit = flops / (main_us * 1e-6) / 1e12, MFMA_PEAK_TFLOPS, "TFLOP/s"
+        achieved_span = flops / (span_us * 1e-6) / 1e12
+    traffic, traffic_commit = traffic_from_profiles(name) if not (args.paged or args.fp8) else (None, None)
     line = {
         "metric": METRIC,
         "value": round(span_us, 3),
@@ -339,8 +401,13 @@ def run(name, args):
                    "rotating_input_sets": rotate, "paged_block_size": args.paged or None,
                    "kv_format": "fp8" if args.fp8 else "bf16"},
         "roofline": {"bound": bound, "achieved": round(achieved, 2), "peak": peak, "unit": unit,
-                     "frac": round(achieved / peak, 4), "traffic": traffic_from_profiles(name),
-                     "kernel": f"sparse_mla_fwd (main), {gbytes} gathered B and {flops} FLOP per launch"},
+                     "frac": round(achieved / peak, 4), "traffic": traffic,
+                     "achieved_span": round(achieved_span, 2), "frac_span": round(achieved_span / peak, 4),
+                     "kernel": (f"sparse_mla_fwd (main), {gbytes} gathered B and {flops} FLOP per launch; "
+                                f"frac on the main kernel's average launch, frac_span on the whole call "
+                                f"(split merge included)"),
+                     "traffic_source": (f"profiles/sparse_mla_fwd_{name}_hbm_traffic.json (build of commit "
+                                        f"{traffic_commit})" if traffic is not None else None)},
         **({"dtype_note": "kv stored as fp8 e4m3 rows; MFMA inputs bf16"} if args.fp8 else {}),
         "breakdown": {
             "span_us": round(span_us, 3),
@@ -464,7 +531,7 @@ def indexer_cpu_baseline(name, data, budget_s=10.0):
             break
     per_call_us = statistics.median(times) * 1e6 * pairs_all / pairs_sample
     return {"value": round(per_call_us, 1), "unit": "µs/call", "cores": torch.get_num_threads(),
-            "kind": "port", "cpu": cpu_model(),
+            "kind": "port", "cpu": cpu_model(), **CPU_COUNTS,
             "sample": (f"FP32 torch indexer logits + numpy top-k oracle on {len(rows)} of {batch * queries} "
                        f"queries of one {name} call, median of {len(times)} runs, scaled by (query, key) pairs")}
 
@@ -540,6 +607,8 @@ def main():
     ap.add_argument("--uv", type=int, default=0, metavar="DV",
                     help="append the W_UV output projection (value head dim DV, e.g. 128) to every call")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-prefill", action="store_true",
+                    help="decode line only (by default it carries a prefill leg: C5 and C4)")
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU oracle timing")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run 5 device copies of MIB MiB (reference kernel for rocprofv3 byte counters)")
@@ -567,10 +636,28 @@ def main():
                 raise SystemExit(f"unknown indexer workload {name!r}")
             print(json.dumps(run_indexer(name, args), ensure_ascii=False), flush=True)
         return
+    threads, counts = cpu_threads()
+    torch.set_num_threads(threads)
+    CPU_COUNTS.update(threads_used=threads, **counts)
     names = ["c2_decode_b8", "c3_decode_h16_mtp", "c4_prefill_h16", "c5_prefill_h128"] if args.all else [args.config]
     for name in names:
         line = run(name, args)
+        if not args.all and not args.no_prefill and BOUND[name] == "hbm":
+            # The metric is "decode B=8 + prefill": the decode line carries the
+            # prefill configurations as a leg of their own (C5 first: the
+            # MFMA-bound headline; C4: 16 heads, L2/MALL-bound).
+            line["prefill"] = {p: prefill_leg(run(p, args, overrides=False))
+                               for p in ("c5_prefill_h128", "c4_prefill_h16")}
         print(json.dumps(line, ensure_ascii=False), flush=True)
+
+
+PREFILL_KEYS = ("value", "unit", "steps", "warmup", "ms_per_step", "config", "roofline", "breakdown", "cpu_baseline")
+
+
+def prefill_leg(line):
+    """The parts of a prefill workload's line that go into the decode line's
+    ``prefill`` object (the rest repeats the decode line's own keys)."""
+    return {k: line[k] for k in PREFILL_KEYS if k in line}
 
 
 if __name__ == "__main__":

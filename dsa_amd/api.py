@@ -170,11 +170,21 @@ def plan_call(shape, config=None, cores: int = 256, kv_fp8: bool = False, w_uv_d
 # stream).  Every call leaves its counters at zero once its kernel completes,
 # so calls in stream order share one array; a call on another stream gets its
 # own.  The arrays hold no inputs or results: only the counters' zeros persist.
+# Hazards of the shared array (also stated in forward's docstring): a stream
+# handle that is destroyed and handed out again while a fused kernel of the
+# old stream still runs would share that kernel's counters; a kernel that does
+# not complete (a device fault ends the process's GPU context anyway) leaves
+# them non-zero.  Callers that want no shared state pass their own counters
+# (forward's ``arrivals``).  Under stream capture every call gets fresh
+# zero-filled counters from the graph's own pool, so each graph records and
+# replays its own fill kernel and graphs never share counters.
 _arrivals_lock = threading.Lock()
 _arrivals = {}
 
 
 def _arrival_counters(device, stream: int, count: int) -> torch.Tensor:
+    if torch.cuda.is_current_stream_capturing():
+        return torch.zeros(count, device=device, dtype=torch.int32)
     key = (device.index, stream)
     with _arrivals_lock:
         buf = _arrivals.get(key)
@@ -184,6 +194,15 @@ def _arrival_counters(device, stream: int, count: int) -> torch.Tensor:
             buf = torch.zeros(size, device=device, dtype=torch.int32)
             _arrivals[key] = buf
         return buf
+
+
+def _check_arrivals(arrivals, device):
+    if arrivals is None:
+        return
+    if not isinstance(arrivals, torch.Tensor) or arrivals.dtype != torch.int32 or arrivals.dim() != 1:
+        raise ValueError("arrivals must be a 1-D int32 tensor")
+    if arrivals.device != device or not arrivals.is_contiguous():
+        raise ValueError("arrivals must be contiguous and on the same ROCm GPU as the other inputs")
 
 
 def _check_w_uv(w_uv, heads: int, device):
@@ -243,7 +262,7 @@ def project_uv(output, w_uv):
 
 
 def forward(q, kv, q_rope, k_rope, indices, *, config=None, cores=None, return_kernels=False,
-            scale=None, block_table=None, w_uv=None):
+            scale=None, block_table=None, w_uv=None, arrivals=None):
     """Sparse MLA attention over given top-k indices.
 
     Returns ``(output, softmax_max, softmax_sum)``: bf16 ``[B,SQ,H,512]`` and
@@ -275,14 +294,29 @@ def forward(q, kv, q_rope, k_rope, indices, *, config=None, cores=None, return_k
     bit.  With a split plan the merge runs in the W_UV launch (also for a
     fused-merge plan: the main kernel then leaves its partials), and the
     latent output is never written.
+
+    ``arrivals`` (int32 ``[n]``, n >= B*SQ*H/heads_per_group, zero before its
+    first use) are the caller's own arrival counters for a fused-merge plan
+    (the last workgroup of each (token, head group) merges the split
+    partials inside the main kernel; every call leaves the counters zero
+    again once its kernel completes, so one tensor serves calls in stream
+    order, and calls that may overlap need tensors of their own).  Without
+    it, calls share one counter array per (device, stream), and a captured
+    call gets counters of its own in the graph's pool.  Ignored by plans that
+    do not fuse the merge.
     """
     scale = _check_scale(scale)
     shape, device, fp8 = _check_inputs(q, kv, q_rope, k_rope, indices, block_table)
     batch, queries, heads, length, topk = shape
     uv = None if w_uv is None else _check_w_uv(w_uv, heads, device)
+    _check_arrivals(arrivals, device)
     if cores is None:
         cores = torch.cuda.get_device_properties(device).multi_processor_count
     config, partials, launches = plan_call(shape, config, cores, fp8, None if uv is None else uv[0])
+    fused = config.fused_merge and config.split > 1 and uv is None
+    groups = batch * queries * (heads // config.bm)
+    if fused and arrivals is not None and arrivals.numel() < groups:
+        raise ValueError(f"arrivals holds {arrivals.numel()} counters; this call needs {groups}")
 
     output = torch.empty_like(q)
     maximum = torch.empty((batch, 1, queries, heads), device=device, dtype=torch.float32)
@@ -303,7 +337,6 @@ def forward(q, kv, q_rope, k_rope, indices, *, config=None, cores=None, return_k
             ptr(output), ptr(maximum), ptr(denominator), ptr(part_o), ptr(part_m), ptr(part_l),
             batch, queries, heads, length, topk)
     merge_uv = uv is not None and config.split > 1
-    fused = config.fused_merge and config.split > 1 and not merge_uv
     with torch.cuda.device(device):
         if merge_uv:
             # Main kernel only; the merge runs inside the W_UV launch below.
@@ -329,7 +362,7 @@ def forward(q, kv, q_rope, k_rope, indices, *, config=None, cores=None, return_k
                 opts.num_blocks = kv.shape[0]
                 opts.block_table = block_table.data_ptr()
             if fused:
-                counters = _arrival_counters(device, stream, batch * queries * (heads // config.bm))
+                counters = arrivals if arrivals is not None else _arrival_counters(device, stream, groups)
                 opts.arrivals = counters.data_ptr()
             rc = _lib.load().dsa_fwd_opts(*args, ctypes.byref(opts), ctypes.byref(plan), ctypes.c_void_p(stream))
     _lib.check(rc, "dsa_fwd_main" if merge_uv else "dsa_fwd")

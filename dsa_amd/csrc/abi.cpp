@@ -280,7 +280,7 @@ int fwd_impl(const uint16_t* q, const uint16_t* kv, const uint16_t* q_rope, cons
     // the paged-kv geometry.
     float scale_log2 = (float)(1.4426950408889634 / 24.0);
     const int32_t* block_table = nullptr;
-    int block_size = 0, max_blocks = 0, kv_rows = L;
+    int block_size = 0, max_blocks = 0, num_blocks = 0, kv_rows = L;
     if (opts) {
         if (opts->kv_format != DSA_KV_BF16 && opts->kv_format != DSA_KV_FP8)
             return fail(-1, "kv_format must be DSA_KV_BF16 (0) or DSA_KV_FP8 (1) (got %d)", opts->kv_format);
@@ -304,7 +304,8 @@ int fwd_impl(const uint16_t* q, const uint16_t* kv, const uint16_t* q_rope, cons
                 return fail(-1, "num_blocks * block_size must be below 33554432 (got %lld)",
                             (long long)opts->num_blocks * block_size);
             if ((uintptr_t)block_table & 3) return fail(-1, "block_table must be 4-byte aligned");
-            kv_rows = opts->num_blocks * block_size;
+            num_blocks = opts->num_blocks;
+            kv_rows = num_blocks * block_size;
         }
     }
     dsa_plan local{};
@@ -356,6 +357,7 @@ int fwd_impl(const uint16_t* q, const uint16_t* kv, const uint16_t* q_rope, cons
     p.block_table = block_table;
     p.block_size = block_size;
     p.max_blocks = max_blocks;
+    p.num_blocks = num_blocks;
     p.kv_rows = kv_rows;
     p.kv_fp8 = fp8 ? 1 : 0;
     p.nsplit = plan->split;

@@ -28,6 +28,7 @@ struct FwdParams {
     // + I % block_size; kv and k_rope are then pools of kv_rows rows.
     const int32_t* block_table;
     int block_size, max_blocks;
+    int num_blocks;          // blocks in the pool (paged); a block entry outside [0, num_blocks) masks its slots
     int kv_rows;             // rows one gather may address: L (contiguous) or the pool size
     int kv_fp8;              // 1: kv holds 656-byte fp8 rows (k_rope unused), narrow variants only
     // Non-NULL (nsplit in [2, 16], narrow variants): one arrival counter per

@@ -294,8 +294,10 @@ __device__ __forceinline__ IdxRegs fetch_indices(const FwdParams& p, const WgCoo
         }
     } else {
         // Second level: the block table row of this batch (again range
-        // checked by the buffer descriptor; an entry outside the pool masks
-        // the slot).
+        // checked by the buffer descriptor).  An entry outside [0, num_blocks)
+        // masks the slot; the test is on the entry itself, so a large entry
+        // cannot wrap the 32-bit row product back into the pool.  Inside the
+        // pool the row is below num_blocks * block_size < 2^25.
         const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
             const_cast<int32_t*>(p.block_table + (int64_t)c.b * p.max_blocks), (short)0, p.max_blocks * 4,
             0x00020000);
@@ -309,9 +311,9 @@ __device__ __forceinline__ IdxRegs fetch_indices(const FwdParams& p, const WgCoo
         for (int i = 0; i < DSA_IDX_CAP / kThreads; ++i) {
             const int s = (int)threadIdx.x + i * kThreads;
             const int id = min(max(raw[i], 0), p.L - 1);
-            const int row = blk[i] * p.block_size + id % p.block_size;
-            const bool ok = (s < nslots) & (c.slot0 + s < p.TOPK) & (raw[i] >= 0) & (raw[i] < p.L) &
-                            (blk[i] >= 0) & (row < p.kv_rows);
+            const bool in_pool = (uint32_t)blk[i] < (uint32_t)p.num_blocks;
+            const int row = (in_pool ? blk[i] : 0) * p.block_size + id % p.block_size;
+            const bool ok = (s < nslots) & (c.slot0 + s < p.TOPK) & (raw[i] >= 0) & (raw[i] < p.L) & in_pool;
             r.v[i] = ok ? row : -1;
         }
     }

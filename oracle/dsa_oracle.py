@@ -237,20 +237,37 @@ def indexer_topk_ref(logits, lengths, topk: int):
 
 
 def accuracy(actual, expected):
-    """Reference metrics (tools/review.py:146-175) of one output tensor pair."""
+    """Reference metrics (tools/review.py:146-175) of one output tensor pair.
+
+    ``max_row_normalized`` is the reference's per-row error
+    (tools/review.py:160-161): for every row of the last dimension,
+    max|delta| / max|expected| over that row, maximised over rows -- per
+    (token, head) over the 512 columns for the output ``[..., H, 512]``, per
+    query over the H heads for softmax_max / softmax_sum ``[B, 1, SQ, H]`` --
+    so one erroneous row cannot hide behind another row's scale.  Rows the
+    oracle left NaN (``reference(tokens=...)``) are skipped.
+    """
     actual = actual.float().cpu()
     expected = expected.float().cpu()
     keep = ~torch.isnan(expected)
     a, e = actual[keep], expected[keep]
     delta = a - e
     ref_max = float(e.abs().max())
+    width = expected.shape[-1]
+    rows_e = expected.reshape(-1, width)
+    rows_a = actual.reshape(-1, width)
+    full = ~torch.isnan(rows_e).any(-1)
+    rows_e, rows_a = rows_e[full], rows_a[full]
+    row_error = (rows_a - rows_e).abs().amax(-1) / rows_e.abs().amax(-1).clamp_min(1e-30)
     return {
         "max_abs": float(delta.abs().max()),
         "reference_max": ref_max,
         "max_normalized": float(delta.abs().max()) / max(ref_max, 1e-30),
+        "max_row_normalized": float(row_error.max()) if row_error.numel() else 0.0,
         "relative_rms": (float(delta.double().square().sum()) / max(float(e.double().square().sum()), 1e-30)) ** 0.5,
         "finite": bool(torch.isfinite(a).all()),
         "elements": int(e.numel()),
+        "rows": int(row_error.numel()),
     }
 
 

@@ -57,7 +57,7 @@ def test_captured_forward_replays_bitwise(shape, config, dv):
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(side):
-        dsa_amd.forward(*data, **kw)  # warm-up on the capture stream: library loaded, counters allocated
+        dsa_amd.forward(*data, **kw)  # warm-up: library loaded, plan cached
     torch.cuda.current_stream().wait_stream(side)
     torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
@@ -76,3 +76,50 @@ def test_captured_forward_replays_bitwise(shape, config, dv):
         print(f"[{tag}] replay {rep}", flush=True)
         for a, b in zip(static_out, eager):
             assert torch.equal(a, b), (tag, rep)
+
+
+def test_two_fused_graphs_replayed_out_of_order():
+    """Two fused-merge calls captured into two graphs (on torch's shared
+    capture stream), then the second graph replayed first and both replayed
+    in turn: each captured call has counters of its own, zero-filled by a
+    kernel recorded in its own graph, so neither replay depends on the other
+    graph having run.  Every replay equals the eager call bit for bit."""
+    config = Tuning(16, 64, 2, kv_waves=4, mfma=16, fused_merge=True)
+    cases = [_case(501, 4, 2, 16), _case(502, 3, 2, 32)]
+    for data in cases:
+        dsa_amd.forward(*data, config=config)
+    torch.cuda.synchronize()
+    graphs, outs = [], []
+    for i, data in enumerate(cases):
+        print(f"[two fused graphs] capture {i}", flush=True)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            outs.append(dsa_amd.forward(*data, config=config))
+        graphs.append(g)
+    torch.cuda.synchronize()
+    eager = [dsa_amd.forward(*data, config=config) for data in cases]
+    torch.cuda.synchronize()
+    for rep, order in enumerate(([1, 0], [1, 1, 0, 0], [0, 1])):
+        for i in order:
+            graphs[i].replay()
+            torch.cuda.synchronize()
+            print(f"[two fused graphs] round {rep} graph {i}", flush=True)
+            for a, b in zip(outs[i], eager[i]):
+                assert torch.equal(a, b), (rep, i)
+
+
+def test_caller_owned_arrivals():
+    """forward(arrivals=...): the caller's counters are used (and left zero),
+    and a too-small tensor is rejected before anything is enqueued."""
+    config = Tuning(16, 64, 2, kv_waves=4, mfma=16, fused_merge=True)
+    data = _case(503, 4, 2, 16)
+    ref = dsa_amd.forward(*data, config=config)
+    own = torch.zeros(4 * 2 * 1, device="cuda", dtype=torch.int32)
+    for _ in range(3):
+        got = dsa_amd.forward(*data, config=config, arrivals=own)
+        torch.cuda.synchronize()
+        for a, b in zip(ref, got):
+            assert torch.equal(a, b)
+        assert int(own.abs().sum()) == 0
+    with pytest.raises(ValueError, match="arrivals"):
+        dsa_amd.forward(*data, config=config, arrivals=own[:7])

@@ -14,6 +14,7 @@ import pytest
 import torch
 
 import dsa_amd
+from _parity import check
 from oracle import dsa_oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -140,8 +141,4 @@ def test_indexer_end_to_end_into_attention():
     kr = torch.randn(B, L, 1, 64, generator=g).bfloat16()
     out, mx, sm = dsa_amd.forward(qa.cuda(), kv.cuda(), qr.cuda(), kr.cuda(), idx)
     torch.cuda.synchronize()
-    ref_o, ref_m, ref_s = O.reference(qa, kv, qr, kr, idx.cpu())
-    acc = O.accuracy(out.cpu(), ref_o)
-    print(f"[indexer -> forward] output N={acc['max_normalized']:.3e}", flush=True)
-    assert acc["max_normalized"] <= 1e-2
-    assert O.rel_error(mx.cpu(), ref_m) <= 1e-4 and O.rel_error(sm.cpu(), ref_s) <= 1e-4
+    check("indexer -> forward", out, mx, sm, O.reference(qa, kv, qr, kr, idx.cpu()))

@@ -14,13 +14,12 @@ import torch
 
 import dsa_amd
 from dsa_amd import Tuning
+from _parity import check
 from oracle import dsa_oracle as O
 
 pytestmark = pytest.mark.gpu
 
 L_MAX = (1 << 25) - 1
-OUT_TOL = 1e-2
-STAT_RTOL = 1e-4
 
 
 @pytest.fixture(scope="module", autouse=True)
@@ -63,12 +62,7 @@ def _compact(ids, L):
 
 
 def _check(tag, got, ref):
-    out, mx, sm = got
-    acc = O.accuracy(out.cpu(), ref[0])
-    em, es = O.rel_error(mx.cpu(), ref[1]), O.rel_error(sm.cpu(), ref[2])
-    print(f"[{tag}] N={acc['max_normalized']:.3e} max rel={em:.2e} sum rel={es:.2e}", flush=True)
-    assert acc["finite"] and acc["max_normalized"] <= OUT_TOL, (tag, acc)
-    assert em <= STAT_RTOL and es <= STAT_RTOL, (tag, em, es)
+    return check(tag, *got, ref)
 
 
 @pytest.mark.parametrize("H,config", [(16, None), (128, Tuning(128, 32, 1, stages=4))], ids=["h16-planner", "h128-wide"])

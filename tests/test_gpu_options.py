@@ -11,12 +11,11 @@ import torch
 
 import dsa_amd
 from dsa_amd import Tuning
+from _parity import check
 from oracle import dsa_oracle as O
 
 pytestmark = pytest.mark.gpu
 
-OUT_TOL = 1e-2
-STAT_RTOL = 1e-4
 PLANS = [None, Tuning(128, 32, 1, stages=4), Tuning(128, 32, 3, stages=4), Tuning(64, 64, 2, kv_waves=2),
          Tuning(32, 64, 1, kv_waves=2, mfma=16), Tuning(16, 64, 3, kv_waves=4, mfma=16)]
 
@@ -67,12 +66,7 @@ def _paged(kv, kr, block_size, seed, holes=0):
 
 
 def _check(tag, out, mx, sm, ref):
-    acc = O.accuracy(out.cpu(), ref[0])
-    em, es = O.rel_error(mx.cpu(), ref[1]), O.rel_error(sm.cpu(), ref[2])
-    print(f"[{tag}] output N={acc['max_normalized']:.3e} max rel={em:.2e} sum rel={es:.2e}", flush=True)
-    assert acc["finite"], tag
-    assert acc["max_normalized"] <= OUT_TOL, (tag, acc)
-    assert em <= STAT_RTOL and es <= STAT_RTOL, (tag, em, es)
+    return check(tag, out, mx, sm, ref)
 
 
 @pytest.mark.parametrize("scale", [192 ** -0.5, 0.03, 1.0 / 24.0])
@@ -114,6 +108,39 @@ def test_paged_holes_are_masked(config):
     for a, b in zip(expect, paged):
         assert torch.equal(a, b)
     _check("paged holes", *paged, O.reference(q, kv, qr, kr, masked))
+
+
+# Block-table entries far outside the pool.  With 64-row blocks the 32-bit
+# row product entry * 64 + offset wraps: (2^26 + 1) * 64 = 2^32 + 64 lands on
+# pool row 64, (2^25 + 1) * 64 and INT32_MAX * 64 turn negative.  Each such
+# slot must be masked like a -1 index (the reference masks by the raw index,
+# dsa/workspace.py:254-257; a row without a block has no data to read).
+FAR_ENTRIES = [2 ** 25 + 1, 2 ** 26 + 1, 2 ** 31 - 1, -(2 ** 31), -2]
+
+
+@pytest.mark.parametrize("config", [None, Tuning(128, 32, 1, stages=4), Tuning(16, 64, 3, kv_waves=4, mfma=16)],
+                         ids=str)
+def test_paged_far_block_entries_are_masked(config):
+    q, kv, qr, kr, ids = _case(8)
+    kv_pool, kr_pool, table = _paged(kv, kr, 64, seed=9)
+    g = torch.Generator().manual_seed(10)
+    flat = table.view(-1)
+    pick = torch.randperm(flat.numel(), generator=g)[: len(FAR_ENTRIES) + 1]
+    for i, v in enumerate(FAR_ENTRIES):
+        flat[pick[i]] = v
+    flat[pick[-1]] = kv_pool.shape[0]  # one past the last block
+    _, _, ok = O.unpage(kv_pool, kr_pool, table)
+    masked = O.mask_unbacked(ids, ok)
+    hit = (masked == -1) & (ids >= 0) & (ids < kv.shape[1])
+    assert int(hit.sum()) > 0, "the far entries must be referenced by some slots"
+    dev = [t.cuda() for t in (q, kv, qr, kr, masked, kv_pool, kr_pool, table, ids)]
+    print(f"[paged far entries {config}] launching ({int(hit.sum())} slots on far blocks)", flush=True)
+    expect = dsa_amd.forward(dev[0], dev[1], dev[2], dev[3], dev[4], config=config)
+    paged = dsa_amd.forward(dev[0], dev[5], dev[2], dev[6], dev[8], config=config, block_table=dev[7])
+    torch.cuda.synchronize()
+    for a, b in zip(expect, paged):
+        assert torch.equal(a, b)
+    _check("paged far entries", *paged, O.reference(q, kv, qr, kr, masked))
 
 
 def test_paged_with_scale_and_split_merge():

@@ -3,8 +3,12 @@ CPU oracle, on the reference's workloads and the MI355X benchmark configs.
 
 Tolerances: output max-normalised error
 max|out - ref| / max|ref| <= 1e-2 against the FP32 oracle; softmax_max and
-softmax_sum relative error <= 1e-4.  The reference's own kernels measured
-N <= 0.0036 on its records; values are printed for the log.
+softmax_sum relative error <= 1e-4.  The reference's per-row error
+(tools/review.py:160-161: per (token, head) over the 512 output columns, per
+query over the heads for max and sum) is gated at the same bounds, so one
+wrong row cannot hide behind another row's scale.  The reference's own
+kernels measured N <= 0.0036 on its records; values are printed for the log.
+Every config C1..C5 is compared on every token.
 """
 import json
 from pathlib import Path
@@ -33,13 +37,17 @@ def _gpu():
 
 def _report(tag, out, mx, sm, ref):
     acc = O.accuracy(out, ref[0])
+    am, asum = O.accuracy(mx, ref[1]), O.accuracy(sm, ref[2])
     em, es = O.rel_error(mx, ref[1]), O.rel_error(sm, ref[2])
-    print(f"[{tag}] output N={acc['max_normalized']:.3e} rms={acc['relative_rms']:.3e} "
-          f"max rel={em:.2e} sum rel={es:.2e}", flush=True)
+    print(f"[{tag}] output N={acc['max_normalized']:.3e} row N={acc['max_row_normalized']:.3e} "
+          f"rms={acc['relative_rms']:.3e} ({acc['rows']} rows) max rel={em:.2e} sum rel={es:.2e} "
+          f"max/sum row N={am['max_row_normalized']:.2e}/{asum['max_row_normalized']:.2e}", flush=True)
     assert acc["finite"], tag
     assert acc["max_normalized"] <= OUT_TOL, (tag, acc)
+    assert acc["max_row_normalized"] <= OUT_TOL, (tag, acc)
     assert em <= STAT_RTOL, (tag, em)
     assert es <= STAT_RTOL, (tag, es)
+    assert am["max_row_normalized"] <= STAT_RTOL and asum["max_row_normalized"] <= STAT_RTOL, (tag, am, asum)
     return acc
 
 
@@ -49,7 +57,7 @@ def _run_and_check(tag, data, config=None, tokens=None):
     out, mx, sm = dsa_amd.forward(*data, config=config)
     torch.cuda.synchronize()
     ref = O.reference(*[t.cpu() for t in data], tokens=tokens)
-    return _report(tag, out.cpu(), mx.cpu(), sm.cpu(), ref), (out, mx, sm)
+    return _report(tag, out.cpu(), mx.cpu(), sm.cpu(), ref), (out, mx, sm), ref
 
 
 # ------------------------------------------------------- reference records
@@ -60,7 +68,7 @@ RECORD_CASES = [r for r in GOLDEN["records"]
 @pytest.mark.parametrize("rec", RECORD_CASES, ids=lambda r: f"{r['case']}-{r['family']}-{r['source'].split('/')[1]}")
 def test_reference_records(rec):
     data = tuple(t.cuda() for t in review_inputs(tuple(rec["shape"]), rec["seed"], rec["family"]))
-    acc, _ = _run_and_check(rec["case"] + "-" + rec["family"], data)
+    acc, _, _ = _run_and_check(rec["case"] + "-" + rec["family"], data)
     # the oracle run here reproduces the record's statistics
     assert acc["reference_max"] == pytest.approx(rec["oracle"]["output"]["reference_max"], rel=1e-5)
 
@@ -90,27 +98,23 @@ def test_c2_full():
     _run_and_check("c2", data)
 
 
-def _subset(name, picks):
-    data = baseline_inputs(name)
-    batch, queries = data[0].shape[:2]
-    tokens = [(b, s) for b, s in picks if b < batch and s < queries]
-    return data, tokens
+def test_c3_full():
+    _run_and_check("c3", baseline_inputs("c3_decode_h16_mtp"))
 
 
-def test_c3_sampled_tokens():
-    data, tokens = _subset("c3_decode_h16_mtp", [(b, s) for b in (0, 1, 17, 40, 63) for s in (0, 1)])
-    _run_and_check("c3", data, tokens=tokens)
+def test_c4_full():
+    _run_and_check("c4", baseline_inputs("c4_prefill_h16"))
 
 
-def test_c4_sampled_tokens():
-    data, tokens = _subset("c4_prefill_h16", [(0, s) for s in (0, 1, 2, 777, 2048, 3000, 4094, 4095)])
-    _run_and_check("c4", data, tokens=tokens)
-
-
-def test_c5_sampled_tokens_per_family():
-    picks = [(0, f * 1024 + s) for f in range(4) for s in (0, 1, 511, 1023)]
-    data, tokens = _subset("c5_prefill_h128", picks)
-    _run_and_check("c5", data, tokens=tokens)
+def test_c5_full():
+    # peaked [0, 1024), duplicates [1024, 2048), invalid [2048, 3072), uniform [3072, 4096)
+    data = baseline_inputs("c5_prefill_h128")
+    _, (out, mx, sm), ref = _run_and_check("c5", data)
+    for f, fam in enumerate(("peaked", "duplicates", "invalid", "uniform")):
+        rows = slice(1024 * f, 1024 * (f + 1))
+        a = O.accuracy(out[:, rows].cpu(), ref[0][:, rows])
+        print(f"[c5-{fam}] output N={a['max_normalized']:.3e} row N={a['max_row_normalized']:.3e}", flush=True)
+        assert a["max_row_normalized"] <= OUT_TOL, (fam, a)
 
 
 # ------------------------------------------------------- plans, edges, invariants

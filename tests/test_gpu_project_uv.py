@@ -164,8 +164,9 @@ def test_forward_w_uv_equals_project_of_output(shape, config, launch):
     # end to end: FP32 oracle attention, then the FP64 projection
     ref = O.project_uv_ref(O.reference(*[t.cpu() for t in data])[0], w)
     acc = O.accuracy(out_v.cpu(), ref)
-    print(f"[{tag}] vs oracle N={acc['max_normalized']:.3e}", flush=True)
+    print(f"[{tag}] vs oracle N={acc['max_normalized']:.3e} row N={acc['max_row_normalized']:.3e}", flush=True)
     assert acc["finite"] and acc["max_normalized"] <= OUT_TOL, (tag, acc)
+    assert acc["max_row_normalized"] <= OUT_TOL, (tag, acc)
 
 
 def test_forward_w_uv_with_scale_paged_and_fp8():

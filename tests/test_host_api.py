@@ -332,3 +332,13 @@ def test_w_uv_rejections(mutate, msg):
 def test_w_uv_strided_value_rows_accepted():
     wkv_b = torch.zeros(16, 128 + 128, 512, dtype=torch.bfloat16)
     assert A._check_w_uv(wkv_b[:, -128:], 16, torch.device("cpu")) == (128, 256 * 512)
+
+
+def test_reference_import_name_is_the_same_operator():
+    # reference callers write `from dsa import forward` (README.md:70 of the reference)
+    import dsa
+    from dsa import CASE_SHAPES as shapes, SELECTED as selected, Tuning as tuning, forward as fwd
+
+    assert fwd is dsa_amd.forward and tuning is dsa_amd.Tuning
+    assert shapes is dsa_amd.CASE_SHAPES and selected is dsa_amd.SELECTED
+    assert set(dsa.__all__) == set(dsa_amd.__all__)

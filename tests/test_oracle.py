@@ -493,3 +493,53 @@ def test_project_uv_linear_and_planted_mistakes_caught():
     wt = torch.randn(3, 512, 512, generator=g).double()
     assert (wrong_head - ref).abs().max() > 1.0
     assert (O.project_uv_ref(x1, wt.transpose(1, 2)) - _uv_brute(x1, wt)).abs().max() > 1.0
+
+
+# ------------------------------------------------------------ per-row metric
+def test_row_metric_hand_worked():
+    # two rows of 4: row 0 scale 8, row 1 scale 0.5; errors 0.04 in row 0,
+    # 0.02 in row 1 -> global N = 0.04 / 8 = 0.005, row N = max(0.005, 0.04)
+    exp = torch.tensor([[8.0, -2.0, 1.0, 0.0], [0.5, -0.25, 0.125, 0.0]])
+    act = exp.clone()
+    act[0, 1] += 0.04
+    act[1, 3] -= 0.02
+    acc = O.accuracy(act, exp)
+    assert acc["max_normalized"] == pytest.approx(0.005, rel=1e-6)
+    assert acc["max_row_normalized"] == pytest.approx(0.04, rel=1e-6)
+    assert acc["rows"] == 2
+
+
+def test_row_metric_catches_error_hidden_by_another_rows_scale():
+    # A whole head row wrong by 100 % at a scale 1000x below the tensor's
+    # maximum: the global normalised error stays near 1e-3 (it would pass a
+    # 1e-2 gate); the per-row metric reports 2.
+    g = torch.Generator().manual_seed(5)
+    exp = torch.randn(2, 3, 16, 512, generator=g)
+    exp[1, 2, 7] *= 1e-3
+    act = exp.clone()
+    act[1, 2, 7] = -exp[1, 2, 7]
+    acc = O.accuracy(act, exp)
+    assert acc["max_normalized"] < 1e-2
+    assert acc["max_row_normalized"] == pytest.approx(2.0, rel=1e-6)
+
+
+def test_row_metric_of_statistics_is_per_query_over_heads():
+    # softmax_max / softmax_sum [B, 1, SQ, H]: a row is one query's H heads
+    exp = torch.tensor([[[[1.0, 2.0, 4.0], [100.0, 50.0, 25.0]]]])
+    act = exp.clone()
+    act[0, 0, 0, 0] = 1.4   # 0.4 / 4 = 0.1 in query 0
+    act[0, 0, 1, 2] = 26.0  # 1 / 100 = 0.01 in query 1
+    acc = O.accuracy(act, exp)
+    assert acc["rows"] == 2
+    assert acc["max_row_normalized"] == pytest.approx(0.1, rel=1e-6)
+    assert acc["max_normalized"] == pytest.approx(0.01, rel=1e-6)
+
+
+def test_row_metric_skips_rows_the_oracle_left_out():
+    exp = torch.full((4, 8), float("nan"))
+    exp[1] = torch.arange(8.0) + 1
+    act = torch.zeros(4, 8)
+    act[1] = exp[1] * 1.01
+    acc = O.accuracy(act, exp)
+    assert acc["rows"] == 1
+    assert acc["max_row_normalized"] == pytest.approx(0.01, rel=1e-5)
