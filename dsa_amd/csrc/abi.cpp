@@ -93,7 +93,8 @@ namespace {
 // read 656-byte fp8 kv rows (the narrow ones) and prices their gathers and
 // per-tile expansion; `fuse` lets it price the in-kernel merge for narrow
 // plans with split <= kMaxFusedSplit.
-int plan_impl(int B, int SQ, int H, int L, int TOPK, int num_cus, bool fp8, bool fuse, dsa_plan* out) {
+int plan_impl(int B, int SQ, int H, int L, int TOPK, int num_cus, bool fp8, bool fuse, int64_t max_partial_bytes,
+              dsa_plan* out) {
     if (!out) return fail(-1, "out is NULL");
     if (int rc = check_shape(B, SQ, H, L, TOPK)) return rc;
     if (num_cus <= 0) return fail(-1, "num_cus must be positive (got %d)", num_cus);
@@ -138,6 +139,9 @@ int plan_impl(int B, int SQ, int H, int L, int TOPK, int num_cus, bool fp8, bool
         for (int split = min_split; split <= ntiles; ++split) {
             const int64_t wgs = groups * split;
             if (wgs > 0x7fffffff) break;
+            if (max_partial_bytes > 0 && split > 1 &&
+                dsa::scratch_partial_bytes(tokens * split * H) > max_partial_bytes)
+                break;  // larger splits need more partials still
             const double rounds = (double)((wgs + num_cus - 1) / num_cus);
             const double tiles = (double)ceil_div(ntiles, split);
             const double wg_us = (kPrologueCycles + tiles * tile_cycles + v.epilogue_cycles) / kClockMHz;
@@ -167,7 +171,11 @@ int plan_impl(int B, int SQ, int H, int L, int TOPK, int num_cus, bool fp8, bool
             }
         }
     }
-    if (best < 0.0) return fail(-1, "no kernel variant for H=%d", H);
+    if (best < 0.0) {
+        if (max_partial_bytes > 0)
+            return fail(-1, "no plan for H=%d whose split partials fit in %lld bytes", H, (long long)max_partial_bytes);
+        return fail(-1, "no kernel variant for H=%d", H);
+    }
     *out = p;
     return dsa_plan_check(out, B, SQ, H, L, TOPK);
 }
@@ -177,14 +185,14 @@ int plan_impl(int B, int SQ, int H, int L, int TOPK, int num_cus, bool fp8, bool
 extern "C" {
 
 int dsa_plan_for(int B, int SQ, int H, int L, int TOPK, int num_cus, dsa_plan* out) {
-    return plan_impl(B, SQ, H, L, TOPK, num_cus, false, true, out);
+    return plan_impl(B, SQ, H, L, TOPK, num_cus, false, true, 0, out);
 }
 
 int dsa_plan_for_opts(int B, int SQ, int H, int L, int TOPK, int num_cus, const dsa_fwd_options* opts,
                       dsa_plan* out) {
     if (opts && opts->kv_format != DSA_KV_BF16 && opts->kv_format != DSA_KV_FP8)
         return fail(-1, "kv_format must be DSA_KV_BF16 (0) or DSA_KV_FP8 (1) (got %d)", opts->kv_format);
-    return plan_impl(B, SQ, H, L, TOPK, num_cus, opts && opts->kv_format == DSA_KV_FP8, true, out);
+    return plan_impl(B, SQ, H, L, TOPK, num_cus, opts && opts->kv_format == DSA_KV_FP8, true, 0, out);
 }
 
 int dsa_partial_elems(const dsa_plan* plan, int B, int SQ, int H, int64_t* part_o_elems,
@@ -265,15 +273,26 @@ int dsa_merge_uv(const float* part_o, const float* part_m, const float* part_l, 
 
 }  // extern "C"
 
-namespace {
+namespace dsa {
 
-// Shared by dsa_fwd and dsa_fwd_main: validate, resolve the plan, launch the
-// main kernel and, when `with_merge` and split > 1, the merge.
-int fwd_impl(const uint16_t* q, const uint16_t* kv, const uint16_t* q_rope, const uint16_t* k_rope,
-             const int32_t* idx, uint16_t* out, float* out_max, float* out_sum, float* part_o, float* part_m,
-             float* part_l, int B, int SQ, int H, int L, int TOPK, const dsa_fwd_options* opts,
-             const dsa_plan* plan, hipStream_t stream, bool with_merge) {
+int64_t scratch_partial_bytes(int64_t rows) {
+    const auto up = [](int64_t b) { return (b + 255) / 256 * 256; };
+    return up(rows * 512 * 4) + 2 * up(rows * 4);
+}
+
+// Shared by every forward entry point: validate, resolve the plan and fill
+// the kernel parameters; nothing is enqueued.  scratch_cap == 0: the caller
+// brings the split partials (and, for the in-kernel merge, arrival counters in
+// opts).  scratch_cap > 0: the partials come from the library's scratch
+// (fwd_scratch.hip), so part_o/part_m/part_l must be NULL; a NULL plan is
+// planned among the splits whose partials fit in scratch_cap bytes, and an
+// explicit plan whose partials do not fit is rejected.
+int fwd_prepare(const uint16_t* q, const uint16_t* kv, const uint16_t* q_rope, const uint16_t* k_rope,
+                const int32_t* idx, uint16_t* out, float* out_max, float* out_sum, float* part_o, float* part_m,
+                float* part_l, int B, int SQ, int H, int L, int TOPK, const dsa_fwd_options* opts,
+                const dsa_plan* plan, bool with_merge, int64_t scratch_cap, FwdCall* call) {
     const bool fp8 = opts && opts->kv_format == DSA_KV_FP8;
+    const bool scratch = scratch_cap > 0;
     if (!q || !kv || !q_rope || (!k_rope && !fp8) || !idx) return fail(-1, "NULL input pointer");
     if (int rc = check_shape(B, SQ, H, L, TOPK)) return rc;
     // Options: scale in log2 units (the default is the reference's 1/24) and
@@ -286,6 +305,7 @@ int fwd_impl(const uint16_t* q, const uint16_t* kv, const uint16_t* q_rope, cons
             return fail(-1, "kv_format must be DSA_KV_BF16 (0) or DSA_KV_FP8 (1) (got %d)", opts->kv_format);
         if (opts->reserved32) return fail(-1, "reserved option fields must be zero");
         if ((uintptr_t)opts->arrivals & 3) return fail(-1, "arrivals must be 4-byte aligned");
+        if (scratch && opts->arrivals) return fail(-1, "arrivals must be NULL here: the counters are in the scratch");
         if (opts->scale != 0.0f) {
             if (!(opts->scale > 0.0f) || !std::isfinite(opts->scale))
                 return fail(-1, "scale must be a positive finite number (got %g)", (double)opts->scale);
@@ -308,6 +328,8 @@ int fwd_impl(const uint16_t* q, const uint16_t* kv, const uint16_t* q_rope, cons
             kv_rows = num_blocks * block_size;
         }
     }
+    if (scratch && (part_o || part_m || part_l))
+        return fail(-1, "part_o, part_m and part_l must be NULL here: the partials are in the scratch");
     dsa_plan local{};
     if (!plan) {
         if (!with_merge) return fail(-1, "dsa_fwd_main needs an explicit plan");
@@ -315,18 +337,25 @@ int fwd_impl(const uint16_t* q, const uint16_t* kv, const uint16_t* q_rope, cons
         int err = (int)hipGetDevice(&dev);
         if (!err) err = (int)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
         if (err) return hip_fail(err, "querying the CU count");
-        if (int rc = plan_impl(B, SQ, H, L, TOPK, cus, fp8, opts && opts->arrivals, &local)) return rc;
+        if (int rc = plan_impl(B, SQ, H, L, TOPK, cus, fp8, scratch || (opts && opts->arrivals), scratch_cap,
+                               &local))
+            return rc;
         plan = &local;
     } else if (int rc = dsa_plan_check(plan, B, SQ, H, L, TOPK)) {
         return rc;
     }
     if (fp8 && plan->mfma != 16) return fail(-1, "fp8 kv rows need a narrow plan (mfma 16)");
     const bool split = plan->split > 1;
-    // The in-kernel merge needs the caller's arrival counters; without them
-    // the merge kernel runs (same bits).
-    const bool fused = split && with_merge && plan->fused_merge && opts && opts->arrivals;
+    const int64_t part_rows = split ? (int64_t)B * SQ * plan->split * H : 0;
+    if (scratch && split && scratch_partial_bytes(part_rows) > scratch_cap)
+        return fail(-1, "split=%d needs %lld bytes of split partials; the scratch holds %lld (pass a plan with a "
+                    "smaller split, or NULL to plan within it, or use dsa_fwd_opts with your own buffers)",
+                    plan->split, (long long)scratch_partial_bytes(part_rows), (long long)scratch_cap);
+    // The in-kernel merge needs arrival counters (the caller's, or the
+    // scratch's); without them the merge kernel runs (same bits).
+    const bool fused = split && with_merge && plan->fused_merge && (scratch || (opts && opts->arrivals));
     if ((!split || with_merge) && (!out || !out_max || !out_sum)) return fail(-1, "NULL output pointer");
-    if (split && (!part_o || !part_m || !part_l))
+    if (split && !scratch && (!part_o || !part_m || !part_l))
         return fail(-1, "split=%d needs part_o, part_m and part_l", plan->split);
     // 16-byte vector accesses need 16-byte aligned rows.
     if (((uintptr_t)q | (uintptr_t)kv | (uintptr_t)q_rope | (uintptr_t)k_rope) & 15)
@@ -336,7 +365,8 @@ int fwd_impl(const uint16_t* q, const uint16_t* kv, const uint16_t* q_rope, cons
     const int64_t rowgroups = (int64_t)B * SQ * plan->split;
     if (rowgroups * (H / plan->heads_per_group) > 0x7fffffff) return fail(-1, "grid too large");
 
-    dsa::FwdParams p{};
+    FwdParams& p = call->p;
+    p = FwdParams{};
     p.q = q;
     p.kv = kv;
     p.q_rope = q_rope;
@@ -364,17 +394,46 @@ int fwd_impl(const uint16_t* q, const uint16_t* kv, const uint16_t* q_rope, cons
     p.ntiles = ceil_div(TOPK, plan->tile_rows);
     p.hgroups = H / plan->heads_per_group;
     p.rowgroups = (int)rowgroups;
-    p.arrivals = fused ? opts->arrivals : nullptr;
+    p.arrivals = fused && !scratch ? opts->arrivals : nullptr;
+    call->plan = *plan;
+    call->split = split;
+    call->fused = fused;
+    call->with_merge = with_merge;
+    call->part_rows = part_rows;
+    return 0;
+}
 
-    int rc = dsa::launch_fwd(p, plan->heads_per_group, plan->kv_waves, plan->tile_rows, plan->stages, plan->mfma,
-                             stream);
+// Enqueue a prepared call: the main kernel and, when it splits and does not
+// merge inside the main kernel, the merge kernel.
+int fwd_enqueue(const FwdCall& c, hipStream_t stream) {
+    const FwdParams& p = c.p;
+    int rc = launch_fwd(p, c.plan.heads_per_group, c.plan.kv_waves, c.plan.tile_rows, c.plan.stages, c.plan.mfma,
+                        stream);
     if (rc) return hip_fail(rc, "main kernel launch");
-    if (split && with_merge && !fused) {
-        rc = dsa::launch_merge(part_o, part_m, part_l, out, out_max, out_sum, B * SQ, H, plan->split, stream);
+    if (c.split && c.with_merge && !c.fused) {
+        rc = launch_merge(p.part_o, p.part_m, p.part_l, p.out, p.out_max, p.out_sum, p.B * p.SQ, p.H, p.nsplit,
+                          stream);
         if (rc) return hip_fail(rc, "merge launch");
     }
     g_err[0] = 0;
     return 0;
+}
+
+int set_error(int code, const char* fmt, const char* detail) { return fail(code, fmt, detail); }
+
+}  // namespace dsa
+
+namespace {
+
+int fwd_impl(const uint16_t* q, const uint16_t* kv, const uint16_t* q_rope, const uint16_t* k_rope,
+             const int32_t* idx, uint16_t* out, float* out_max, float* out_sum, float* part_o, float* part_m,
+             float* part_l, int B, int SQ, int H, int L, int TOPK, const dsa_fwd_options* opts,
+             const dsa_plan* plan, hipStream_t stream, bool with_merge) {
+    dsa::FwdCall call;
+    if (int rc = dsa::fwd_prepare(q, kv, q_rope, k_rope, idx, out, out_max, out_sum, part_o, part_m, part_l, B, SQ,
+                                  H, L, TOPK, opts, plan, with_merge, 0, &call))
+        return rc;
+    return dsa::fwd_enqueue(call, stream);
 }
 
 }  // namespace

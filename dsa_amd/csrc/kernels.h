@@ -5,6 +5,8 @@
 #include <stdint.h>
 #include <hip/hip_runtime_api.h>
 
+#include "../../include/dsa_mi355x.h"
+
 namespace dsa {
 
 // Everything one launch of the main kernel needs, passed by value as the
@@ -41,6 +43,33 @@ struct FwdParams {
     int hgroups;             // H / heads_per_group
     int rowgroups;           // tokens * nsplit
 };
+
+// A validated forward call (abi.cpp: fwd_prepare), ready to enqueue.
+struct FwdCall {
+    FwdParams p;
+    dsa_plan plan;
+    bool split, fused, with_merge;
+    int64_t part_rows;  // rows of the split partials (B * SQ * split * H; 0 without a split)
+};
+
+// Bytes the split partials of `rows` rows take in the scratch layout
+// (part_o, part_m, part_l, each 256-byte aligned).
+int64_t scratch_partial_bytes(int64_t rows);
+
+// Validate a forward call and resolve its plan (nothing is enqueued); see
+// abi.cpp.  scratch_cap > 0: the partials will come from the library's
+// scratch of that many bytes (part_* must be NULL).
+int fwd_prepare(const uint16_t* q, const uint16_t* kv, const uint16_t* q_rope, const uint16_t* k_rope,
+                const int32_t* idx, uint16_t* out, float* out_max, float* out_sum, float* part_o, float* part_m,
+                float* part_l, int B, int SQ, int H, int L, int TOPK, const dsa_fwd_options* opts,
+                const dsa_plan* plan, bool with_merge, int64_t scratch_cap, FwdCall* call);
+
+// Enqueue a prepared call; returns the ABI status (0, or a hipError_t with
+// dsa_last_error set).
+int fwd_enqueue(const FwdCall& call, hipStream_t stream);
+
+// Set dsa_last_error to fmt (one %s: detail) and return code.
+int set_error(int code, const char* fmt, const char* detail);
 
 // Kernel variants compiled into the library, keyed by
 // (heads_per_group, kv_waves, tile_rows, stages, mfma).

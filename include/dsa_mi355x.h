@@ -17,7 +17,8 @@
  *   - plain pointers to device memory; bf16 tensors are passed as uint16_t
  *     bit patterns; all tensors dense row-major (contiguous);
  *   - the library allocates and frees nothing, and keeps no state across calls
- *     other than read-only kernel handles;
+ *     other than read-only kernel handles and, for dsa_fwd_noalloc only, its
+ *     static scratch array (below);
  *   - work is enqueued on `stream`, a hipStream_t passed as void* (NULL = the
  *     default stream); no call synchronises the device.  The header needs no
  *     HIP header, so C and FFI callers include it on its own;
@@ -216,6 +217,33 @@ int dsa_fwd_main_opts(const uint16_t* q, const uint16_t* kv, const uint16_t* q_r
                       float* part_o, float* part_m, float* part_l,
                       int B, int SQ, int H, int L, int TOPK,
                       const dsa_fwd_options* opts, const dsa_plan* plan, void* stream);
+
+/*
+ * dsa_fwd_opts for callers that cannot allocate: code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc.  No
+ * counterpart in the reference (its forward allocates the partials with
+ * torch.empty on every call, dsa/api.py:101-113).
+ *
+ * Same arguments and results as dsa_fwd_opts without part_o / part_m /
+ * part_l: the split partials -- and the arrival counters of a plan with
+ * fused_merge = 1 -- live in a static device array of the library (one per
+ * GPU, held until the process ends) whose partial region is
+ * DSA_NOALLOC_PARTIAL_BYTES bytes.  opts->arrivals must be NULL.  A call
+ * whose partials, B * SQ * split * H * (512 + 2) * 4 bytes (each of the three
+ * arrays 256-byte aligned), exceed it is rejected (< 0, nothing enqueued);
+ * plan == NULL plans among the splits that fit.  The call allocates and
+ * frees nothing (no hipMalloc, hipFree or allocating library routine).  The
+ * first call on a GPU also enqueues one small kernel that zeroes the
+ * counters.  Every call on a GPU shares that GPU's array and leaves its last
+ * partials there: calls that can overlap on one GPU (other streams,
+ * concurrently replayed graphs) race on it.
+ */
+#define DSA_NOALLOC_PARTIAL_BYTES (32 * 1024 * 1024)
+int dsa_fwd_noalloc(const uint16_t* q, const uint16_t* kv, const uint16_t* q_rope,
+                    const uint16_t* k_rope, const int32_t* idx,
+                    uint16_t* out, float* out_max, float* out_sum,
+                    int B, int SQ, int H, int L, int TOPK,
+                    const dsa_fwd_options* opts, const dsa_plan* plan, void* stream);
 
 /*
  * FP32 merge of split partials (dsa/merge.py:13-91):
