@@ -352,7 +352,9 @@ def run(name, args, overrides=True):
         bm, split, kv_waves, mfma = v[:4]
         bn, stages = (v[4], v[5]) if len(v) > 4 else (64, 2)
         fused = bool(v[6]) if len(v) > 6 else False
-        config = Tuning(bm, bn, split, kv_waves=kv_waves, stages=stages, mfma=mfma, fused_merge=fused)
+        pv_cols = v[7] if len(v) > 7 else 512
+        config = Tuning(bm, bn, split, kv_waves=kv_waves, stages=stages, mfma=mfma, fused_merge=fused,
+                        pv_cols=pv_cols)
     print(f"[bench] {name} shape={shape} plan={config} rotate={rotate}", file=sys.stderr, flush=True)
     sets = [baseline_inputs(name, seed=args.seed + i, device="cuda", cpu_recipe=False) for i in range(rotate)]
     if args.fp8:  # the same inputs with kv and k_rope written as 656-byte fp8 rows
@@ -596,7 +598,8 @@ def main():
     ap.add_argument("--config", default="c2_decode_b8", choices=sorted(BASELINE_CONFIGS))
     ap.add_argument("--all", action="store_true", help="one line per configuration C2..C5")
     ap.add_argument("--rotate", type=int, default=0, help="input sets to cycle (default per workload)")
-    ap.add_argument("--plan", default="", help="override the plan: bm,split,kv_waves,mfma[,bn,stages[,fused]]")
+    ap.add_argument("--plan", default="",
+                    help="override the plan: bm,split,kv_waves,mfma[,bn,stages[,fused[,pv_cols]]]")
     ap.add_argument("--seed", type=int, default=20261102)
     ap.add_argument("--paged", type=int, default=0, metavar="BLOCK",
                     help="run the workload on paged kv (block pools of BLOCK rows, random block table)")

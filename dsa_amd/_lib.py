@@ -27,7 +27,7 @@ class DsaPlan(ctypes.Structure):
         ("stages", ctypes.c_int32),
         ("mfma", ctypes.c_int32),
         ("fused_merge", ctypes.c_int32),
-        ("reserved", ctypes.c_int32),
+        ("pv_cols", ctypes.c_int32),
     ]
 
 

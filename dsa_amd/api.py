@@ -149,7 +149,7 @@ def plan_call(shape, config=None, cores: int = 256, kv_fp8: bool = False, w_uv_d
             raise ValueError("fp8 kv rows need a narrow plan (mfma=16)")
     batch, queries, heads, _, _ = shape
     tokens = batch * queries
-    variant = "wide" if config.mfma == 32 else "narrow"
+    variant = "xp" if config.pv_cols == 128 else ("wide" if config.mfma == 32 else "narrow")
     launches = [Launch(f"sparse_mla_fwd_{variant}_h{config.bm}_kw{config.kv_waves}_bn{config.bn}_s{config.stages}",
                        tokens * config.split * (heads // config.bm), 256, _LDS_BYTES)]
     partials = None

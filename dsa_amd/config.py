@@ -16,6 +16,11 @@ Ascend Cube/Vector pipeline; here the plan describes gfx950 workgroups:
 * ``fused_merge`` -- with split in [2, 16] on a narrow plan (mfma 16), the
                   main kernel's last workgroup per (token, head group) merges
                   the partials: one launch instead of two, the same bits.
+* ``pv_cols``  -- output columns one wave computes in PV (the reference's
+                  Tuning.pv_cols): 512 (each wave: all columns for its own
+                  rows) or 128 (the four waves split a 64-row tile's rows for
+                  QK, exchange P through LDS and split the columns for PV;
+                  mfma 16, kv_waves 4, bm 16, 32 or 64).
 
 Unlike the reference, shapes outside the table are accepted: the library's
 planner (``dsa_plan_for``) derives a plan for any supported shape.
@@ -39,18 +44,20 @@ class Tuning:
     stages: int = 2
     mfma: int = 32
     fused_merge: bool = False
+    pv_cols: int = 512
 
     def to_c(self) -> _lib.DsaPlan:
         p = _lib.DsaPlan()
         p.heads_per_group, p.tile_rows, p.split = self.bm, self.bn, self.split
         p.kv_waves, p.stages, p.mfma = self.kv_waves, self.stages, self.mfma
         p.fused_merge = 1 if self.fused_merge else 0
+        p.pv_cols = self.pv_cols
         return p
 
     @staticmethod
     def from_c(p: _lib.DsaPlan) -> "Tuning":
         return Tuning(p.heads_per_group, p.tile_rows, p.split, p.kv_waves, p.stages, p.mfma,
-                      bool(p.fused_merge))
+                      bool(p.fused_merge), p.pv_cols if p.pv_cols else 512)
 
 
 # (batch, query length, heads, KV length, number of selected indices).
@@ -103,7 +110,7 @@ def check_tuning(config: Tuning, shape) -> None:
     if not isinstance(config, Tuning):
         raise TypeError("config must be a dsa_amd.Tuning")
     if any(type(v) is not int
-           for v in (config.bm, config.bn, config.split, config.kv_waves, config.stages, config.mfma)):
+           for v in (config.bm, config.bn, config.split, config.kv_waves, config.stages, config.mfma, config.pv_cols)):
         raise ValueError("Tuning fields must be int")
     if type(config.fused_merge) is not bool:
         raise ValueError("Tuning.fused_merge must be a bool")
@@ -113,33 +120,36 @@ def check_tuning(config: Tuning, shape) -> None:
 
 
 # Per-shape plans for MI355X (256 CUs), the counterpart of the reference's
-# table (dsa/config.py:42-59): the library planner's choice (dsa_plan_for, a
-# cost model fitted to MI355X measurements), except where a measured sweep
-# found a faster plan (decode_b32, prefill_q16, prefill_q64, decode_b4_h128).
-# The in-kernel merge pays where a (token, head group) has little to merge
-# (2 splits x 16 heads: C3 69.3 -> 65.3 µs); with 512 KiB groups (C1, C2)
-# one CU reading them back costs more than the merge kernel.
+# table (dsa/config.py:42-59): the fastest plan of a measured sweep over
+# every variant (narrow, wide, column-split PV) and split around 128-512
+# workgroups, per shape; the library planner (dsa_plan_for, a cost model
+# fitted to the same measurements) covers every other shape.  The
+# column-split PV variants (pv_cols=128) won every 16- and 32-head plan
+# (2-15 % over pv_cols=512); the in-kernel merge pays where a (token, head
+# group) has little to merge (2 splits x 16 heads).
+_XP16 = dict(kv_waves=4, mfma=16, pv_cols=128)
+_XP32 = dict(kv_waves=4, mfma=16, pv_cols=128)
 SELECTED = {
-    "decode_b1": Tuning(16, 64, 16, kv_waves=4, mfma=16),
-    "decode_b8": Tuning(32, 64, 8, kv_waves=2, mfma=16),
-    "decode_b32": Tuning(32, 64, 2, kv_waves=2, mfma=16),
-    "decode_tp8": Tuning(16, 64, 16, kv_waves=4, mfma=16),
-    "prefill_q16": Tuning(32, 64, 4, kv_waves=2, mfma=16),
-    "prefill_q64": Tuning(32, 64, 1, kv_waves=2, mfma=16),
-    "prefill_tp8": Tuning(16, 64, 2, kv_waves=4, mfma=16, fused_merge=True),
-    "prefill_k512": Tuning(32, 64, 1, kv_waves=2, mfma=16),
-    "decode_b4_h128": Tuning(16, 64, 8, kv_waves=4, mfma=16),
+    "decode_b1": Tuning(16, 64, 16, **_XP16),
+    "decode_b8": Tuning(16, 64, 4, **_XP16),
+    "decode_b32": Tuning(64, 64, 4, kv_waves=1, mfma=16),
+    "decode_tp8": Tuning(16, 64, 16, **_XP16),
+    "prefill_q16": Tuning(32, 64, 4, **_XP32),
+    "prefill_q64": Tuning(32, 64, 1, **_XP32),
+    "prefill_tp8": Tuning(16, 64, 2, fused_merge=True, **_XP16),
+    "prefill_k512": Tuning(32, 64, 1, **_XP32),
+    "decode_b4_h128": Tuning(16, 64, 8, **_XP16),
     "prefill_b4_h128": Tuning(128, 32, 1, stages=4),
-    "decode_b4_h64": Tuning(16, 64, 16, kv_waves=4, mfma=16),
+    "decode_b4_h64": Tuning(16, 64, 16, **_XP16),
     "prefill_b4_h64": Tuning(64, 64, 1, kv_waves=2),
-    "decode_b4_h32": Tuning(16, 64, 16, kv_waves=4, mfma=16),
-    "prefill_b4_h32": Tuning(32, 64, 1, kv_waves=2, mfma=16),
-    "decode_b4_h16": Tuning(16, 64, 16, kv_waves=4, mfma=16),
-    "prefill_b4_h16": Tuning(16, 64, 1, kv_waves=4, mfma=16),
-    "c1_decode_b1": Tuning(16, 64, 16, kv_waves=4, mfma=16),
-    "c2_decode_b8": Tuning(32, 64, 8, kv_waves=2, mfma=16),
-    "c3_decode_h16_mtp": Tuning(16, 64, 2, kv_waves=4, mfma=16, fused_merge=True),
-    "c4_prefill_h16": Tuning(16, 64, 1, kv_waves=4, mfma=16),
+    "decode_b4_h32": Tuning(16, 64, 16, **_XP16),
+    "prefill_b4_h32": Tuning(32, 64, 1, **_XP32),
+    "decode_b4_h16": Tuning(16, 64, 32, **_XP16),
+    "prefill_b4_h16": Tuning(16, 64, 1, **_XP16),
+    "c1_decode_b1": Tuning(16, 64, 16, **_XP16),
+    "c2_decode_b8": Tuning(16, 64, 4, **_XP16),
+    "c3_decode_h16_mtp": Tuning(16, 64, 2, fused_merge=True, **_XP16),
+    "c4_prefill_h16": Tuning(16, 64, 1, **_XP16),
     "c5_prefill_h128": Tuning(128, 32, 1, stages=4),
 }
 _BY_SHAPE = {}

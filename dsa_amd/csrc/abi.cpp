@@ -65,22 +65,27 @@ int dsa_plan_check(const dsa_plan* plan, int B, int SQ, int H, int L, int TOPK) 
         return fail(-1, "heads_per_group must be a positive multiple of mfma=%d (got %d)", mfma, hpg);
     if (H % hpg) return fail(-1, "heads_per_group %d must divide H=%d", hpg, H);
     if (bn != 32 && bn != 64) return fail(-1, "tile_rows must be 32 or 64 (got %d)", bn);
-    if (plan->kv_waves * (hpg / mfma) != 4)
+    const int pv_cols = plan->pv_cols == 0 ? 512 : plan->pv_cols;
+    if (pv_cols != 512 && pv_cols != 128) return fail(-1, "pv_cols must be 0 (= 512), 512 or 128 (got %d)", pv_cols);
+    if (pv_cols == 512 && plan->kv_waves * (hpg / mfma) != 4)
         return fail(-1, "kv_waves * heads_per_group / mfma must be 4 (got kv_waves=%d)", plan->kv_waves);
-    if (!dsa::fwd_variant_exists(hpg, plan->kv_waves, bn, plan->stages, mfma))
-        return fail(-1, "no kernel variant for heads_per_group=%d kv_waves=%d tile_rows=%d stages=%d mfma=%d", hpg,
-                    plan->kv_waves, bn, plan->stages, mfma);
+    if (!dsa::fwd_variant_exists(hpg, plan->kv_waves, bn, plan->stages, mfma, pv_cols))
+        return fail(-1,
+                    "no kernel variant for heads_per_group=%d kv_waves=%d tile_rows=%d stages=%d mfma=%d pv_cols=%d",
+                    hpg, plan->kv_waves, bn, plan->stages, mfma, pv_cols);
     const int ntiles = ceil_div(TOPK, bn);
     if (split < 1 || split > ntiles)
         return fail(-1, "split must be in [1, %d] for TOPK=%d (got %d)", ntiles, TOPK, split);
-    if (ceil_div(ntiles, split) * bn > DSA_IDX_CAP)
-        return fail(-1, "split %d leaves more than %d slots per workgroup (TOPK=%d)", split, DSA_IDX_CAP, TOPK);
+    const int cap = dsa::fwd_index_cap(hpg, pv_cols);
+    if (ceil_div(ntiles, split) * bn > cap)
+        return fail(-1, "split %d leaves more than %d slots per workgroup (TOPK=%d)", split, cap, TOPK);
     if (plan->fused_merge != 0 && plan->fused_merge != 1)
         return fail(-1, "fused_merge must be 0 or 1 (got %d)", plan->fused_merge);
-    if (plan->fused_merge && (mfma != 16 || split > kMaxFusedSplit))
-        return fail(-1, "fused_merge needs a narrow plan (mfma 16) with split <= %d (got mfma=%d split=%d)",
-                    kMaxFusedSplit, mfma, split);
-    if (plan->reserved) return fail(-1, "plan reserved field must be zero");
+    if (plan->fused_merge && (mfma != 16 || split > kMaxFusedSplit || (pv_cols == 128 && hpg != 16)))
+        return fail(-1,
+                    "fused_merge needs a narrow plan (mfma 16; with pv_cols 128, 16 heads per group) with split <= %d "
+                    "(got mfma=%d split=%d heads_per_group=%d pv_cols=%d)",
+                    kMaxFusedSplit, mfma, split, hpg, pv_cols);
     g_err[0] = 0;
     return 0;
 }
@@ -109,16 +114,23 @@ int plan_impl(int B, int SQ, int H, int L, int TOPK, int num_cus, bool fp8, bool
     // workgroup of each group reads the group's partials back on one CU
     // (measured ≈30 GB/s: C3's 64 KiB groups cost ≈0.4 µs over the main
     // kernel, C1's and C2's 512 KiB groups 17-18 µs).
+    // The column-split PV variants (pv_cols 128) replace narrow<2,2> and
+    // narrow<1,4> on bf16 rows: measured 2-15 % faster on every shape swept
+    // (no row-wave exchange in the epilogue); fp8 rows are read by the
+    // narrow variants only.
     struct Variant {
-        int hpg, kvw, bn, stages, mfma;
+        int hpg, kvw, bn, stages, mfma, pv_cols;
+        bool bf16, fp8;
         double tile_cycles, epilogue_cycles;
     };
     static const Variant kVariants[] = {
-        {128, 1, 32, 4, 32, 4400.0, 18000.0},  // wide<4,1,32,4>
-        {64, 2, 64, 2, 32, 5000.0, 15000.0},   // wide<2,2,64,2>
-        {64, 1, 64, 2, 16, 7000.0, 6000.0},    // narrow<4,1>
-        {32, 2, 64, 2, 16, 4000.0, 10000.0},   // narrow<2,2>
-        {16, 4, 64, 2, 16, 2800.0, 10000.0},   // narrow<1,4>
+        {128, 1, 32, 4, 32, 512, true, false, 4400.0, 18000.0},  // wide<4,1,32,4>
+        {64, 2, 64, 2, 32, 512, true, false, 5000.0, 15000.0},   // wide<2,2,64,2>
+        {64, 1, 64, 2, 16, 512, true, true, 7000.0, 6000.0},     // narrow<4,1>
+        {32, 2, 64, 2, 16, 512, false, true, 4000.0, 10000.0},   // narrow<2,2>
+        {16, 4, 64, 2, 16, 512, false, true, 2800.0, 10000.0},   // narrow<1,4>
+        {32, 4, 64, 2, 16, 128, true, false, 3800.0, 6000.0},    // xp<2>: 32 heads, column-split PV
+        {16, 4, 64, 2, 16, 128, true, false, 2700.0, 4000.0},    // xp<1>: 16 heads, column-split PV
     };
     constexpr double kClockMHz = 2200.0, kPrologueCycles = 9000.0, kLaunchUs = 2.0;
     constexpr double kHbmBytesPerUs = 4.8e6, kCuBytesPerUs = 3.0e4;                // sustained gather rates
@@ -131,10 +143,10 @@ int plan_impl(int B, int SQ, int H, int L, int TOPK, int num_cus, bool fp8, bool
     dsa_plan p{};
     for (const Variant& v : kVariants) {
         if (H % v.hpg) continue;
-        if (fp8 && v.mfma != 16) continue;
+        if (fp8 ? !v.fp8 : !v.bf16) continue;
         const double tile_cycles = v.tile_cycles + (fp8 ? kFp8TileCycles : 0.0);
         const int ntiles = ceil_div(TOPK, v.bn);
-        const int min_split = ceil_div(ntiles * v.bn, DSA_IDX_CAP);
+        const int min_split = ceil_div(ntiles * v.bn, dsa::fwd_index_cap(v.hpg, v.pv_cols));
         const int64_t groups = tokens * (H / v.hpg);
         for (int split = min_split; split <= ntiles; ++split) {
             const int64_t wgs = groups * split;
@@ -167,7 +179,7 @@ int plan_impl(int B, int SQ, int H, int L, int TOPK, int num_cus, bool fp8, bool
             if (best < 0.0 || cost < best * 0.999) {
                 best = cost;
                 p.heads_per_group = v.hpg, p.kv_waves = v.kvw, p.tile_rows = v.bn, p.stages = v.stages;
-                p.mfma = v.mfma, p.split = split, p.fused_merge = fused;
+                p.mfma = v.mfma, p.split = split, p.fused_merge = fused, p.pv_cols = v.pv_cols;
             }
         }
     }
@@ -344,7 +356,8 @@ int fwd_prepare(const uint16_t* q, const uint16_t* kv, const uint16_t* q_rope, c
     } else if (int rc = dsa_plan_check(plan, B, SQ, H, L, TOPK)) {
         return rc;
     }
-    if (fp8 && plan->mfma != 16) return fail(-1, "fp8 kv rows need a narrow plan (mfma 16)");
+    if (fp8 && (plan->mfma != 16 || (plan->pv_cols != 0 && plan->pv_cols != 512)))
+        return fail(-1, "fp8 kv rows need a narrow plan (mfma 16, pv_cols 512)");
     const bool split = plan->split > 1;
     const int64_t part_rows = split ? (int64_t)B * SQ * plan->split * H : 0;
     if (scratch && split && scratch_partial_bytes(part_rows) > scratch_cap)
@@ -408,7 +421,7 @@ int fwd_prepare(const uint16_t* q, const uint16_t* kv, const uint16_t* q_rope, c
 int fwd_enqueue(const FwdCall& c, hipStream_t stream) {
     const FwdParams& p = c.p;
     int rc = launch_fwd(p, c.plan.heads_per_group, c.plan.kv_waves, c.plan.tile_rows, c.plan.stages, c.plan.mfma,
-                        stream);
+                        c.plan.pv_cols == 0 ? 512 : c.plan.pv_cols, stream);
     if (rc) return hip_fail(rc, "main kernel launch");
     if (c.split && c.with_merge && !c.fused) {
         rc = launch_merge(p.part_o, p.part_m, p.part_l, p.out, p.out_max, p.out_sum, p.B * p.SQ, p.H, p.nsplit,

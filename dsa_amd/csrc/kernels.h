@@ -72,15 +72,19 @@ int fwd_enqueue(const FwdCall& call, hipStream_t stream);
 int set_error(int code, const char* fmt, const char* detail);
 
 // Kernel variants compiled into the library, keyed by
-// (heads_per_group, kv_waves, tile_rows, stages, mfma).
-bool fwd_variant_exists(int heads_per_group, int kv_waves, int tile_rows, int stages, int mfma);
+// (heads_per_group, kv_waves, tile_rows, stages, mfma, pv_cols).
+bool fwd_variant_exists(int heads_per_group, int kv_waves, int tile_rows, int stages, int mfma, int pv_cols);
+
+// Slots of the index cache of one workgroup of a variant (DSA_IDX_CAP, or
+// half of it where the LDS holds more per tile).
+int fwd_index_cap(int heads_per_group, int pv_cols);
 
 // Grid size (workgroups) of the main kernel for these params/plan.
 int64_t fwd_grid(const FwdParams& p);
 
 // Enqueue the main kernel; returns a hipError_t.
 int launch_fwd(const FwdParams& p, int heads_per_group, int kv_waves, int tile_rows,
-               int stages, int mfma, hipStream_t stream);
+               int stages, int mfma, int pv_cols, hipStream_t stream);
 
 // Enqueue the split merge; returns a hipError_t.
 int launch_merge(const float* part_o, const float* part_m, const float* part_l,

@@ -266,11 +266,13 @@ __device__ __forceinline__ WgCoords wg_coords(const FwdParams& p) {
 // the padding of a ragged last tile; nslots <= DSA_IDX_CAP, checked on the
 // host).  Split into a global-load half and an LDS-store half so other loads
 // can be issued in between without waiting for these.
+template <int CAP = DSA_IDX_CAP>
 struct IdxRegs {
-    int v[DSA_IDX_CAP / kThreads];
+    static_assert(CAP % kThreads == 0 && CAP <= DSA_IDX_CAP, "index cache size");
+    int v[CAP / kThreads];
 };
-template <int BN>
-__device__ __forceinline__ IdxRegs fetch_indices(const FwdParams& p, const WgCoords& c) {
+template <int BN, int CAP = DSA_IDX_CAP>
+__device__ __forceinline__ IdxRegs<CAP> fetch_indices(const FwdParams& p, const WgCoords& c) {
     // Buffer loads over the token's index row: a slot past TOPK reads 0
     // (hardware range check) and is then masked.  Being intrinsics rather
     // than plain loads, they are never turned into branches around each load,
@@ -278,16 +280,17 @@ __device__ __forceinline__ IdxRegs fetch_indices(const FwdParams& p, const WgCoo
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<int32_t*>(p.idx + (int64_t)c.token * p.TOPK), (short)0, p.TOPK * 4, 0x00020000);
     const int nslots = c.nt * BN;
-    int raw[DSA_IDX_CAP / kThreads];
+    constexpr int N = CAP / kThreads;
+    int raw[N];
 #pragma unroll
-    for (int i = 0; i < DSA_IDX_CAP / kThreads; ++i)
+    for (int i = 0; i < N; ++i)
         raw[i] = __builtin_amdgcn_raw_buffer_load_b32(rs, (c.slot0 + (int)threadIdx.x + i * kThreads) * 4, 0, 0);
     // Cached value: the kv row to gather (the pool row when paged), or -1 for
     // a masked slot (index < 0 or >= L, slot past TOPK or past the range).
-    IdxRegs r;
+    IdxRegs<CAP> r;
     if (p.block_table == nullptr) {
 #pragma unroll
-        for (int i = 0; i < DSA_IDX_CAP / kThreads; ++i) {
+        for (int i = 0; i < N; ++i) {
             const int s = (int)threadIdx.x + i * kThreads;
             const bool ok = (s < nslots) & (c.slot0 + s < p.TOPK) & (raw[i] >= 0) & (raw[i] < p.L);
             r.v[i] = ok ? raw[i] : -1;
@@ -301,14 +304,14 @@ __device__ __forceinline__ IdxRegs fetch_indices(const FwdParams& p, const WgCoo
         const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
             const_cast<int32_t*>(p.block_table + (int64_t)c.b * p.max_blocks), (short)0, p.max_blocks * 4,
             0x00020000);
-        int blk[DSA_IDX_CAP / kThreads];
+        int blk[N];
 #pragma unroll
-        for (int i = 0; i < DSA_IDX_CAP / kThreads; ++i) {
+        for (int i = 0; i < N; ++i) {
             const int id = min(max(raw[i], 0), p.L - 1);
             blk[i] = __builtin_amdgcn_raw_buffer_load_b32(rb, (id / p.block_size) * 4, 0, 0);
         }
 #pragma unroll
-        for (int i = 0; i < DSA_IDX_CAP / kThreads; ++i) {
+        for (int i = 0; i < N; ++i) {
             const int s = (int)threadIdx.x + i * kThreads;
             const int id = min(max(raw[i], 0), p.L - 1);
             const bool in_pool = (uint32_t)blk[i] < (uint32_t)p.num_blocks;
@@ -322,9 +325,10 @@ __device__ __forceinline__ IdxRegs fetch_indices(const FwdParams& p, const WgCoo
 // Every entry of the cache is written (slots past the range hold -1): a
 // conditional store would let the compiler sink each global load into its
 // branch and wait for it there, serialising the loads.
-__device__ __forceinline__ void store_indices(const IdxRegs& r, uint32_t idx_lds) {
+template <int CAP>
+__device__ __forceinline__ void store_indices(const IdxRegs<CAP>& r, uint32_t idx_lds) {
 #pragma unroll
-    for (int i = 0; i < DSA_IDX_CAP / kThreads; ++i)
+    for (int i = 0; i < CAP / kThreads; ++i)
         lds_store<int>(idx_lds + 4 * ((int)threadIdx.x + i * kThreads), r.v[i]);
 }
 
@@ -406,7 +410,7 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd_wide(FwdParams p) 
 
     // Index loads first: the first gather depends on them, Q only on the
     // first MFMA.
-    const IdxRegs ids = fetch_indices<BN>(p, c);
+    const IdxRegs<> ids = fetch_indices<BN>(p, c);
 
     // ---- Q fragments: B operand of S^T = K . Q^T.  Lane holds
     // Q[head][16*ks + 8*h .. +7]; ks 32..35 come from q_rope.
@@ -955,7 +959,7 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd_narrow(FwdParams p
 
     // Index loads first: the first gather depends on them, Q only on the
     // first MFMA.
-    const IdxRegs ids = fetch_indices<kBN>(p, c);
+    const IdxRegs<> ids = fetch_indices<kBN>(p, c);
 
     // ---- Q fragments: lane holds Q[head][128*g + 8*ks .. +7]; ks 16, 17 from
     // q_rope (dims 32*(ks-16) + 8*g).
@@ -1306,6 +1310,336 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd_narrow(FwdParams p
     }
 }
 
+// ============================================================ column-split PV
+// pv_cols = 128.  The four waves split each 64-row tile's ROWS for QK and the
+// softmax (wave w: rows 16 w .. 16 w + 15), exchange the bf16 P tile through
+// LDS, and split the 512 output COLUMNS for PV (wave w: columns 128 w ..
+// 128 w + 127, over all 64 rows of the tile).  A wave holds HB head blocks of
+// 16 (v_mfma_f32_16x16x32_bf16; each K and V fragment read from LDS serves all
+// HB blocks), so every gathered element is read from LDS once for QK and once
+// for PV whatever the head count; PV runs with k = 32 rows (full MFMA rate); and
+// no O accumulators are exchanged at the end, each wave owning its own output
+// columns.  The four waves share one reference max per head, fixed from the
+// first tile with a valid row (the restart logic of the other variants applies
+// unchanged to it).
+template <int HB>
+struct XpLds {
+    static constexpr int BM = 16 * HB;
+    static constexpr int RING = 2 * 64 * 1152;
+    static constexpr int IDX_CAP = HB <= 2 ? DSA_IDX_CAP : DSA_IDX_CAP / 2;
+    static constexpr int IDX_OFF = RING;
+    // P of one tile, per head 64 bf16 in the k order of the PV B operand
+    // (position 32 kk + 8 g + 4 a + j holds row 32 kk + 16 a + 4 g + j), heads
+    // 144 bytes apart.
+    static constexpr int P_STRIDE = 144;
+    static constexpr int P_OFF = IDX_OFF + IDX_CAP * 4;
+    static constexpr int MX_OFF = P_OFF + BM * P_STRIDE;  // [4 waves][BM] floats
+    static constexpr int FLAG_OFF = MX_OFF + kWaves * BM * 4;
+    static constexpr int LDS_BYTES = FLAG_OFF + 16;
+    static_assert(LDS_BYTES <= 160 * 1024, "LDS budget");
+    static_assert(2 * kWaves * BM * 4 <= RING, "epilogue exchange fits the ring");
+};
+
+template <int HB>
+__global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd_xp(FwdParams p) {
+    using R = Ring<64, 2>;
+    using X = XpLds<HB>;
+    constexpr int kBN = 64;
+    __shared__ __attribute__((aligned(1024))) char smem[X::LDS_BYTES];
+    const uint32_t lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)smem;
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int g = lane >> 4;
+    const int n16 = lane & 15;
+
+    const WgCoords c = wg_coords<kBN>(p);
+    const int head0 = c.hgi * X::BM;
+    const IdxRegs<X::IDX_CAP> ids = fetch_indices<kBN, X::IDX_CAP>(p, c);
+
+    // ---- Q fragments of the HB head blocks (as in the narrow variant):
+    // lane holds Q[head][128 g + 8 ks .. + 7]; ks 16, 17 from q_rope.
+    bf16x8 qf[HB][18];
+#pragma unroll
+    for (int hb = 0; hb < HB; ++hb) {
+        const int head = head0 + hb * 16 + n16;
+        const uint16_t* qrow = p.q + ((int64_t)c.token * p.H + head) * 512 + 128 * g;
+#pragma unroll
+        for (int ks = 0; ks < 16; ++ks) qf[hb][ks] = *reinterpret_cast<const bf16x8*>(qrow + 8 * ks);
+        const uint16_t* rrow = p.q_rope + ((int64_t)c.token * p.H + head) * 64 + 8 * g;
+        qf[hb][16] = *reinterpret_cast<const bf16x8*>(rrow);
+        qf[hb][17] = *reinterpret_cast<const bf16x8*>(rrow + 32);
+    }
+
+    const uint32_t idx_lds = lds + X::IDX_OFF;
+    store_indices(ids, idx_lds);
+    lds_barrier();
+    const Gather gt = make_gather(p, c.b);
+
+    // QK A operand: row 16 wave + n16, logical chunk 16 g + ks (sw_kv depends
+    // on the row mod 16 only).
+    const uint32_t qk_g = (uint32_t)g << 8;
+    const uint32_t qk_x = (uint32_t)sw_kv(n16) << 4;
+    uint32_t rp_off[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) rp_off[j] = ((4 * j + g) ^ sw_rope(n16)) << 4;
+    // PV A operand (transposed reads, as in the narrow variant) restricted to
+    // this wave's 256-byte column window.
+    const int tr_row = 4 * g + (n16 >> 2);
+    uint32_t tr_off[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+        tr_off[j] = ((((2 * j + ((n16 & 3) >> 1)) ^ sw_kv(tr_row)) << 4) + ((n16 & 1) << 3)) + ((uint32_t)wave << 8);
+    // P exchange: this wave writes rows 16 wave + 4 g .. + 3 of head n16 (8
+    // bytes) and reads positions 32 kk + 8 g .. + 7 (16 bytes) for the PV B
+    // operand.
+    const uint32_t p_base = lds + X::P_OFF + (uint32_t)n16 * X::P_STRIDE;
+    const uint32_t p_wr = p_base + (uint32_t)(32 * (wave >> 1) + 8 * g + 4 * (wave & 1)) * 2;
+    const uint32_t p_rd = p_base + (uint32_t)(8 * g) * 2;
+    const uint32_t mx_lds = lds + X::MX_OFF;
+    const uint32_t flag_lds = lds + X::FLAG_OFF;
+
+    // ---- running state, per head block (log2 units)
+    f32x4 oacc[HB][8];
+    float m_ref[HB], m_true[HB], l_run[HB];
+#pragma unroll
+    for (int hb = 0; hb < HB; ++hb) m_ref[hb] = m_true[hb] = -FLT_MAX;
+
+#pragma unroll 1
+    for (int pass = 0; pass < 2; ++pass) {
+#pragma unroll
+        for (int hb = 0; hb < HB; ++hb) {
+#pragma unroll
+            for (int cb = 0; cb < 8; ++cb) oacc[hb][cb] = f32x4{0.f, 0.f, 0.f, 0.f};
+            l_run[hb] = 0.f;
+        }
+        bool ref_set = pass == 1;  // pass 1 runs against the exact max (set at the vote)
+        bool overflow = false;
+        issue_tile<R>(p, gt, 0, R::stage(lds, 0), idx_lds, wave, lane);
+        wait_vmcnt<0>();  // Q and tile 0
+
+        for (int t = 0; t < c.nt; ++t) {
+            if (t > 0) wait_vmcnt<0>();  // this wave's gathers of tile t
+            lds_barrier();                // tile t complete; stage of tile t - 1, P and MX free
+            if (t + 1 < c.nt) issue_tile<R>(p, gt, t + 1, R::stage(lds, t + 1), idx_lds, wave, lane);
+            const uint32_t stage = R::stage(lds, t);
+
+            // ---- S^T = K . Q^T for this wave's 16 rows and HB head blocks.
+            const i32x4 iv = lds_load<i32x4>(idx_lds + 4 * (t * kBN + 16 * wave + 4 * g));
+            const uint32_t krow = stage + (uint32_t)(16 * wave + n16) * 1024;
+            auto kfrag = [&](int ks) -> bf16x8 {
+                if (ks < 16) return lds_load<bf16x8>(krow + qk_g + ((uint32_t)(16 * ks) ^ qk_x));
+                return lds_load<bf16x8>(stage + R::KV_BYTES + (16 * wave + n16) * 128 + rp_off[ks - 16]);
+            };
+            constexpr int NCH = HB == 1 ? 2 : 1;
+            f32x4 sacc[HB][NCH];
+#pragma unroll
+            for (int hb = 0; hb < HB; ++hb)
+#pragma unroll
+                for (int ch = 0; ch < NCH; ++ch) sacc[hb][ch] = f32x4{0.f, 0.f, 0.f, 0.f};
+            {
+                bf16x8 kf[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) kf[j] = kfrag(j);
+#pragma unroll
+                for (int ks = 0; ks < 18; ++ks) {
+                    const int ch = NCH == 2 ? (ks & 1) : 0;
+#pragma unroll
+                    for (int hb = 0; hb < HB; ++hb)
+                        sacc[hb][ch] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[ks & 3], qf[hb][ks], sacc[hb][ch], 0, 0, 0);
+                    if (ks + 4 < 18) kf[ks & 3] = kfrag(ks + 4);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            }
+
+            // ---- scale, mask, max over this wave's rows; lane holds rows
+            // 16 wave + 4 g + r (r = 0..3) of head hb * 16 + n16.
+            float x[HB][4], lmax[HB];
+#pragma unroll
+            for (int hb = 0; hb < HB; ++hb) {
+                f32x4 sres = sacc[hb][0];
+                if constexpr (NCH == 2) sres += sacc[hb][1];
+                lmax[hb] = -INFINITY;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    x[hb][r] = iv[r] >= 0 ? sres[r] : -INFINITY;
+                    lmax[hb] = fmaxf(lmax[hb], x[hb][r]);
+                }
+                lmax[hb] = max_xor32(max_xor16(lmax[hb])) * p.score_scale_log2;
+                m_true[hb] = fmaxf(m_true[hb], lmax[hb]);
+            }
+            if (!ref_set) {
+                // The first tile with a valid row fixes the shared reference
+                // max: the tile's max per head over all four waves.
+                if (g == 0)
+#pragma unroll
+                    for (int hb = 0; hb < HB; ++hb) lds_store<float>(mx_lds + 4 * (wave * X::BM + hb * 16 + n16), lmax[hb]);
+                lds_barrier();
+                float tmax[HB];
+#pragma unroll
+                for (int hb = 0; hb < HB; ++hb) {
+                    tmax[hb] = -INFINITY;
+#pragma unroll
+                    for (int w = 0; w < kWaves; ++w)
+                        tmax[hb] = fmaxf(tmax[hb], lds_load<float>(mx_lds + 4 * (w * X::BM + hb * 16 + n16)));
+                }
+                // a tile either has a valid row (every head's max is finite) or not
+                if (__builtin_amdgcn_readfirstlane(__float_as_int(tmax[0])) != __float_as_int(-INFINITY)) {
+#pragma unroll
+                    for (int hb = 0; hb < HB; ++hb) m_ref[hb] = tmax[hb];
+                    ref_set = true;
+                }
+            }
+            bool ovf = false;
+#pragma unroll
+            for (int hb = 0; hb < HB; ++hb) ovf |= lmax[hb] > m_ref[hb] + kRestartLog2;
+            overflow |= ovf;
+            bf16x4 pb[HB];
+            const bool clamp = __any(ovf);
+#pragma unroll
+            for (int hb = 0; hb < HB; ++hb) {
+                const float neg_ref = -m_ref[hb];
+                float psum = 0.f;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const float a = fmaf(x[hb][r], p.score_scale_log2, neg_ref);
+                    const float e = fast_exp2(clamp ? fminf(a, kRestartLog2) : a);
+                    psum += e;
+                    pb[hb][r] = (__bf16)e;
+                }
+                l_run[hb] += psum;
+                lds_store<bf16x4>(p_wr + hb * 16 * X::P_STRIDE, pb[hb]);
+            }
+            lds_barrier();  // P of all four waves
+
+            // ---- O^T[cols of this wave] += V^T . P^T over the tile's 64 rows:
+            // 2 k-steps x 8 column blocks, each V fragment used by HB MFMAs.
+            bf16x8 pk[HB][2];
+#pragma unroll
+            for (int hb = 0; hb < HB; ++hb)
+#pragma unroll
+                for (int kk = 0; kk < 2; ++kk)
+                    pk[hb][kk] = lds_load<bf16x8>(p_rd + hb * 16 * X::P_STRIDE + kk * 64);
+            auto vfrag = [&](int step) -> bf16x8 {
+                const int kk = step >> 3, cb = step & 7;
+                const uint32_t r0a = stage + (uint32_t)(32 * kk + tr_row) * 1024 + tr_off[cb];
+                const bf16x4 v0 = lds_load_tr(r0a);
+                const bf16x4 v1 = lds_load_tr(r0a + 16 * 1024);
+                return __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7);
+            };
+            constexpr int PV_DEPTH = 4;
+            bf16x8 vf[PV_DEPTH];
+#pragma unroll
+            for (int j = 0; j < PV_DEPTH; ++j) vf[j] = vfrag(j);
+#pragma unroll
+            for (int step = 0; step < 16; ++step) {
+                const int kk = step >> 3, cb = step & 7;
+#pragma unroll
+                for (int hb = 0; hb < HB; ++hb)
+                    oacc[hb][cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf[step % PV_DEPTH], pk[hb][kk], oacc[hb][cb], 0, 0, 0);
+                if (step + PV_DEPTH < 16) vf[step % PV_DEPTH] = vfrag(step + PV_DEPTH);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+
+        // ---- workgroup vote: does any head need pass 1?
+        if (pass == 1) break;
+        if (threadIdx.x == 0) lds_store<int>(flag_lds, 0);
+        lds_barrier();  // also: every wave is past its last ring and P read
+        if (__any(overflow) && lane == 0) lds_store<int>(flag_lds, 1);
+        lds_barrier();
+        if (__builtin_amdgcn_readfirstlane(lds_load<int>(flag_lds)) == 0) break;
+        // pass 1 runs against the exact max over all waves
+        if (g == 0)
+#pragma unroll
+            for (int hb = 0; hb < HB; ++hb) lds_store<float>(mx_lds + 4 * (wave * X::BM + hb * 16 + n16), m_true[hb]);
+        lds_barrier();
+#pragma unroll
+        for (int hb = 0; hb < HB; ++hb) {
+            float mt = -FLT_MAX;
+#pragma unroll
+            for (int w = 0; w < kWaves; ++w) mt = fmaxf(mt, lds_load<float>(mx_lds + 4 * (w * X::BM + hb * 16 + n16)));
+            m_ref[hb] = mt;
+        }
+        lds_barrier();  // MX read by every wave before any tile writes it again
+    }
+
+    // ---- epilogue: sum l and take the max over the four waves' rows (the ring
+    // is free once every wave is past its last read).
+    lds_barrier();
+    const uint32_t l_lds = lds, mt_lds = lds + kWaves * X::BM * 4;
+#pragma unroll
+    for (int hb = 0; hb < HB; ++hb) {
+        l_run[hb] = sum_xor32(sum_xor16(l_run[hb]));
+        if (g == 0) {
+            lds_store<float>(l_lds + 4 * (wave * X::BM + hb * 16 + n16), l_run[hb]);
+            lds_store<float>(mt_lds + 4 * (wave * X::BM + hb * 16 + n16), m_true[hb]);
+        }
+    }
+    lds_barrier();
+    int eln = lane;
+    asm volatile("" : "+v"(eln));
+    const int eg = eln >> 4, en16 = eln & 15;
+#pragma unroll
+    for (int hb = 0; hb < HB; ++hb) {
+        float lt = 0.f, mt = -FLT_MAX;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) {
+            lt += lds_load<float>(l_lds + 4 * (w * X::BM + hb * 16 + en16));
+            mt = fmaxf(mt, lds_load<float>(mt_lds + 4 * (w * X::BM + hb * 16 + en16)));
+        }
+        l_run[hb] = lt;
+        m_true[hb] = mt;
+    }
+    const bool writes_ml = wave == 0 && eg == 0;
+    if (p.nsplit == 1) {
+#pragma unroll
+        for (int hb = 0; hb < HB; ++hb) {
+            const int head = head0 + hb * 16 + en16;
+            const float inv_l = 1.0f / l_run[hb];  // O and l share m_ref
+            uint16_t* orow = p.out + ((int64_t)c.token * p.H + head) * 512 + 128 * wave + 4 * eg;
+#pragma unroll
+            for (int cb = 0; cb < 8; ++cb)
+                store_bf16x4(orow + 16 * cb, oacc[hb][cb][0] * inv_l, oacc[hb][cb][1] * inv_l, oacc[hb][cb][2] * inv_l,
+                             oacc[hb][cb][3] * inv_l);
+            if (writes_ml) {
+                p.out_max[(int64_t)c.token * p.H + head] = m_true[hb] * kLn2;
+                p.out_sum[(int64_t)c.token * p.H + head] = l_run[hb] * fast_exp2(m_ref[hb] - m_true[hb]);
+            }
+        }
+    } else if (HB > 1 || p.arrivals == nullptr) {
+#pragma unroll
+        for (int hb = 0; hb < HB; ++hb) {
+            const int head = head0 + hb * 16 + en16;
+            const float to_true = fast_exp2(m_ref[hb] - m_true[hb]);
+            const int64_t prow = ((int64_t)c.token * p.nsplit + c.sp) * p.H + head;
+            float* orow = p.part_o + prow * 512 + 128 * wave + 4 * eg;
+#pragma unroll
+            for (int cb = 0; cb < 8; ++cb) *reinterpret_cast<f32x4*>(orow + 16 * cb) = oacc[hb][cb] * to_true;
+            if (writes_ml) {
+                p.part_m[prow] = m_true[hb] * kLn2;
+                p.part_l[prow] = l_run[hb] * to_true;
+            }
+        }
+    } else {
+        // In-kernel merge (one head block): the same partials, stored
+        // agent-coherent; the last workgroup of the (token, head group) merges.
+        const float to_true = fast_exp2(m_ref[0] - m_true[0]);
+        const __amdgpu_buffer_rsrc_t rs = group_block(p, c.token, c.sp, head0, 16);
+        const uint32_t voff = (uint32_t)(en16 * 2048 + 16 * eg + 64 * 8 * wave);
+#pragma unroll
+        for (int cb = 0; cb < 8; ++cb)
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, oacc[0][cb] * to_true), rs, voff + 64 * cb,
+                                                   0, kAgentCoherent);
+        if (writes_ml) {
+            const int64_t prow = ((int64_t)c.token * p.nsplit + c.sp) * p.H + head0 + en16;
+            __hip_atomic_store(p.part_m + prow, m_true[0] * kLn2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(p.part_l + prow, l_run[0] * to_true, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        merge_if_last<8>(p, c, head0, 16, en16, eg, writes_ml, 8 * wave, flag_lds);
+    }
+}
+
 template <typename K>
 int launch(K kernel, const FwdParams& p, hipStream_t stream) {
     hipLaunchKernelGGL(kernel, dim3((unsigned)fwd_grid(p)), dim3(kThreads), 0, stream, p);
@@ -1314,7 +1648,10 @@ int launch(K kernel, const FwdParams& p, hipStream_t stream) {
 
 }  // namespace
 
-bool fwd_variant_exists(int hpg, int kvw, int bn, int stages, int mfma) {
+bool fwd_variant_exists(int hpg, int kvw, int bn, int stages, int mfma, int pv_cols) {
+    if (pv_cols == 128)  // column-split PV: four waves, 64-row tiles, 16, 32 or 64 heads
+        return mfma == 16 && kvw == 4 && bn == 64 && stages == 2 && (hpg == 16 || hpg == 32 || hpg == 64);
+    if (pv_cols != 512) return false;
     if (mfma == 32)
         return (hpg == 128 && kvw == 1 && bn == 32 && stages == 4) || (hpg == 64 && kvw == 2 && bn == 64 && stages == 2);
     if (mfma == 16 && bn == 64 && stages == 2)
@@ -1324,9 +1661,19 @@ bool fwd_variant_exists(int hpg, int kvw, int bn, int stages, int mfma) {
 
 int64_t fwd_grid(const FwdParams& p) { return (int64_t)p.rowgroups * p.hgroups; }
 
-int launch_fwd(const FwdParams& p, int hpg, int kvw, int bn, int stages, int mfma, hipStream_t stream) {
-    if (!fwd_variant_exists(hpg, kvw, bn, stages, mfma)) return (int)hipErrorInvalidValue;
-    if (p.kv_fp8 && mfma != 16) return (int)hipErrorInvalidValue;  // fp8 rows: narrow variants only
+int fwd_index_cap(int hpg, int pv_cols) {
+    if (pv_cols == 128 && hpg == 64) return XpLds<4>::IDX_CAP;
+    return DSA_IDX_CAP;
+}
+
+int launch_fwd(const FwdParams& p, int hpg, int kvw, int bn, int stages, int mfma, int pv_cols, hipStream_t stream) {
+    if (!fwd_variant_exists(hpg, kvw, bn, stages, mfma, pv_cols)) return (int)hipErrorInvalidValue;
+    if (p.kv_fp8 && (mfma != 16 || pv_cols != 512)) return (int)hipErrorInvalidValue;  // fp8 rows: narrow variants only
+    if (pv_cols == 128) {
+        if (hpg == 16) return launch(sparse_mla_fwd_xp<1>, p, stream);
+        if (hpg == 32) return launch(sparse_mla_fwd_xp<2>, p, stream);
+        return launch(sparse_mla_fwd_xp<4>, p, stream);
+    }
     if (mfma == 32) {
         if (hpg == 128) return launch(sparse_mla_fwd_wide<4, 1, 32, 4>, p, stream);
         return launch(sparse_mla_fwd_wide<2, 2, 64, 2>, p, stream);

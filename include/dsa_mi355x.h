@@ -66,7 +66,15 @@ extern "C" {
  *                     dsa_fwd_options.arrivals; otherwise (dsa_fwd, or no
  *                     arrivals) the merge kernel runs.  Same bits either way.
  *                     No effect when split == 1.
- *   reserved        : must be zero.
+ *   pv_cols         : output columns one wave computes in PV (the reference's
+ *                     Tuning.pv_cols, dsa/config.py:10-19): 0 or 512 -- each
+ *                     wave computes all 512 columns for its own rows (the
+ *                     variants above) -- or 128: the four waves split each
+ *                     64-row tile's rows for QK and the softmax, exchange the
+ *                     bf16 P tile through LDS and split the 512 output columns
+ *                     for PV (mfma 16, kv_waves 4, tile_rows 64, stages 2,
+ *                     heads_per_group 16, 32 or 64; with 64 heads a workgroup
+ *                     holds at most 1024 slots).
  */
 typedef struct dsa_plan {
     int32_t heads_per_group;
@@ -76,7 +84,7 @@ typedef struct dsa_plan {
     int32_t stages;
     int32_t mfma;
     int32_t fused_merge;
-    int32_t reserved;
+    int32_t pv_cols;
 } dsa_plan;
 
 /* Library version, (major << 16) | minor. */

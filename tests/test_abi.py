@@ -42,7 +42,7 @@ def test_version_and_last_error():
 
 def test_struct_layout_matches_header():
     assert ctypes.sizeof(_lib.DsaPlan) == 32
-    assert _lib.DsaPlan.fused_merge.offset == 24 and _lib.DsaPlan.reserved.offset == 28
+    assert _lib.DsaPlan.fused_merge.offset == 24 and _lib.DsaPlan.pv_cols.offset == 28
     # float, 3 x int32, pointer, 2 x int32, pointer
     assert ctypes.sizeof(_lib.DsaFwdOptions) == 40
     assert _lib.DsaFwdOptions.block_table.offset == 16
@@ -134,7 +134,8 @@ def test_fused_merge_plan_checks():
     for bad, msg in ((_lib.DsaPlan(32, 64, 8, 2, 2, 16, 2), b"0 or 1"),
                      (_lib.DsaPlan(64, 64, 4, 2, 2, 32, 1), b"narrow"),      # wide variant
                      (_lib.DsaPlan(32, 64, 17, 2, 2, 16, 1), b"split <= 16"),
-                     (_lib.DsaPlan(32, 64, 8, 2, 2, 16, 0, 1), b"reserved")):
+                     (_lib.DsaPlan(32, 64, 8, 4, 2, 16, 1, 128), b"16 heads per group"),  # column-split PV, 32 heads
+                     (_lib.DsaPlan(32, 64, 8, 2, 2, 16, 0, 1), b"pv_cols")):
         assert lib.dsa_plan_check(ctypes.byref(bad), *shape) < 0
         assert msg in lib.dsa_last_error(), lib.dsa_last_error()
     # misaligned arrival counters are rejected before any launch
@@ -289,3 +290,30 @@ def test_header_is_plain_c_and_links(tmp_path):
     assert int(version) == _lib.load().dsa_version() and int(rc) == 0 and int(split) >= 1
     assert (int(po) > 0) == (int(split) > 1) and int(pml) * 512 == int(po)
     assert int(bad) < 0 and "NULL" in " ".join(msg)
+
+
+def test_column_split_pv_plan_checks():
+    """pv_cols = 128 (the reference's Tuning.pv_cols): four waves, 64-row
+    tiles, 16 / 32 / 64 heads per group; 0 means 512."""
+    lib = _lib.load()
+    shape = (8, 1, 128, 32768, 2048)
+    for hpg in (16, 32, 64):
+        ok = _lib.DsaPlan(hpg, 64, 8, 4, 2, 16, 0, 128)
+        assert lib.dsa_plan_check(ctypes.byref(ok), *shape) == 0, lib.dsa_last_error()
+    assert lib.dsa_plan_check(ctypes.byref(_lib.DsaPlan(16, 64, 8, 4, 2, 16, 1, 128)), *shape) == 0
+    assert lib.dsa_plan_check(ctypes.byref(_lib.DsaPlan(32, 64, 8, 2, 2, 16, 0, 512)), *shape) == 0
+    for bad in (_lib.DsaPlan(32, 64, 8, 2, 2, 16, 0, 128),     # kv_waves must be 4
+                _lib.DsaPlan(128, 32, 8, 4, 4, 32, 0, 128),    # wide
+                _lib.DsaPlan(32, 64, 8, 4, 2, 16, 0, 256)):    # 256 is not a variant
+        assert lib.dsa_plan_check(ctypes.byref(bad), *shape) < 0
+    # 64 heads: at most 1024 slots per workgroup, so TOPK 2048 needs split >= 2
+    assert lib.dsa_plan_check(ctypes.byref(_lib.DsaPlan(64, 64, 1, 4, 2, 16, 0, 128)), *shape) < 0
+    assert b"1024 slots" in lib.dsa_last_error()
+    assert lib.dsa_plan_check(ctypes.byref(_lib.DsaPlan(64, 64, 2, 4, 2, 16, 0, 128)), *shape) == 0
+    # fp8 rows are read by the pv_cols 512 narrow variants only
+    fake = ctypes.c_void_p(1 << 20)
+    o = _lib.DsaFwdOptions(kv_format=_lib.KV_FP8)
+    plan = _lib.DsaPlan(16, 64, 1, 4, 2, 16, 0, 128)
+    assert lib.dsa_fwd_opts(fake, fake, fake, fake, fake, fake, fake, fake, None, None, None, 1, 1, 16, 4096, 64,
+                            ctypes.byref(o), ctypes.byref(plan), None) < 0
+    assert b"pv_cols 512" in lib.dsa_last_error()

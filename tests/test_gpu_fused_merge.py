@@ -8,6 +8,7 @@ against the FP32 oracle.  The arrival counters must be back at zero after
 every call.
 """
 import ctypes
+import dataclasses
 
 import pytest
 import torch
@@ -46,7 +47,7 @@ def _case(seed, B=2, SQ=3, H=128, L=4096, K=2048, masked_tail=False):
 
 
 def _fused(cfg: Tuning) -> Tuning:
-    return Tuning(cfg.bm, cfg.bn, cfg.split, cfg.kv_waves, cfg.stages, cfg.mfma, True)
+    return dataclasses.replace(cfg, fused_merge=True)
 
 
 def _counters_zero():
@@ -62,7 +63,8 @@ def _check_oracle(tag, out, mx, sm, ref):
 PLANS = [Tuning(16, 64, 2, kv_waves=4, mfma=16), Tuning(16, 64, 3, kv_waves=4, mfma=16),
          Tuning(16, 64, 5, kv_waves=4, mfma=16), Tuning(16, 64, 16, kv_waves=4, mfma=16),
          Tuning(32, 64, 2, kv_waves=2, mfma=16), Tuning(32, 64, 8, kv_waves=2, mfma=16),
-         Tuning(64, 64, 4, kv_waves=1, mfma=16), Tuning(64, 64, 7, kv_waves=1, mfma=16)]
+         Tuning(64, 64, 4, kv_waves=1, mfma=16), Tuning(64, 64, 7, kv_waves=1, mfma=16),
+         Tuning(16, 64, 2, kv_waves=4, mfma=16, pv_cols=128), Tuning(16, 64, 5, kv_waves=4, mfma=16, pv_cols=128)]
 
 
 @pytest.mark.parametrize("config", PLANS, ids=str)

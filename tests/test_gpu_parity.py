@@ -123,7 +123,11 @@ PLANS_H128 = [Tuning(128, 32, 1, stages=4), Tuning(128, 32, 3, stages=4), Tuning
               Tuning(64, 64, 32, kv_waves=2),
               Tuning(64, 64, 1, mfma=16), Tuning(64, 64, 32, mfma=16),
               Tuning(32, 64, 1, kv_waves=2, mfma=16), Tuning(32, 64, 5, kv_waves=2, mfma=16),
-              Tuning(16, 64, 1, kv_waves=4, mfma=16), Tuning(16, 64, 32, kv_waves=4, mfma=16)]
+              Tuning(16, 64, 1, kv_waves=4, mfma=16), Tuning(16, 64, 32, kv_waves=4, mfma=16),
+              # column-split PV (pv_cols 128): 16, 32 and 64 heads per group
+              Tuning(16, 64, 1, kv_waves=4, mfma=16, pv_cols=128), Tuning(16, 64, 9, kv_waves=4, mfma=16, pv_cols=128),
+              Tuning(32, 64, 1, kv_waves=4, mfma=16, pv_cols=128), Tuning(32, 64, 5, kv_waves=4, mfma=16, pv_cols=128),
+              Tuning(64, 64, 2, kv_waves=4, mfma=16, pv_cols=128), Tuning(64, 64, 7, kv_waves=4, mfma=16, pv_cols=128)]
 
 
 @pytest.mark.parametrize("config", PLANS_H128, ids=str)
