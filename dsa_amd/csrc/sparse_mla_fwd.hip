@@ -641,7 +641,38 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd_wide(FwdParams p) 
     const float to_true = fast_exp2(m_ref - m_true);
     const float l_fin = l_run * to_true;
     const float m_nat = m_true * kLn2;
-    if (p.nsplit == 1) {
+    if (p.nsplit == 1 && KW == 1) {
+        // The bf16 rows of all 32 * HW heads go through the (now idle) ring
+        // first, so that every global store instruction writes one head's
+        // whole 1 KiB row: a lane holds 4 columns of each of 16 column blocks
+        // of one head, a scattered 8-byte pattern in memory.
+        constexpr int HROW = 1040;  // bytes per staged head row (1 KiB + 16: spreads heads over the banks)
+        static_assert(HW * 32 * HROW <= R::IDX_OFF, "staged rows fit the ring");
+        const float inv_l = 1.0f / l_run;  // O and l_run share m_ref
+        lds_barrier();                     // every wave is past its last ring read
+        const uint32_t srow = lds + (uint32_t)((hw * 32 + en32) * HROW + 8 * eh);
+#pragma unroll
+        for (int cb = 0; cb < 16; ++cb)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                bf16x4 v;
+                v[0] = (__bf16)(oacc[cb][4 * q] * inv_l);
+                v[1] = (__bf16)(oacc[cb][4 * q + 1] * inv_l);
+                v[2] = (__bf16)(oacc[cb][4 * q + 2] * inv_l);
+                v[3] = (__bf16)(oacc[cb][4 * q + 3] * inv_l);
+                lds_store<bf16x4>(srow + 2 * (32 * cb + 8 * q), v);
+            }
+        if (eh == 0) {
+            p.out_max[(int64_t)c.token * p.H + ehead] = m_nat;
+            p.out_sum[(int64_t)c.token * p.H + ehead] = l_fin;
+        }
+        lds_barrier();
+        // wave w stores head rows w, w + 4, ...: 64 lanes x 16 bytes = one row
+        uint16_t* obase = p.out + ((int64_t)c.token * p.H + c.hgi * (32 * HW)) * 512 + 8 * eln;
+#pragma unroll 4
+        for (int hr = wave; hr < HW * 32; hr += kWaves)
+            *reinterpret_cast<bf16x8*>(obase + (int64_t)hr * 512) = lds_load<bf16x8>(lds + hr * HROW + 16 * eln);
+    } else if (p.nsplit == 1) {
         const float inv_l = 1.0f / l_run;  // O and l_run share m_ref
         uint16_t* orow = p.out + ((int64_t)c.token * p.H + ehead) * 512 + 4 * eh;
 #pragma unroll
@@ -1593,20 +1624,38 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd_xp(FwdParams p) {
     }
     const bool writes_ml = wave == 0 && eg == 0;
     if (p.nsplit == 1) {
+        // bf16 rows staged in the ring past the l / max exchange, then stored
+        // one whole 1 KiB head row per instruction (a lane holds 4 columns of
+        // 8 column blocks: 8-byte pieces 32 bytes apart in memory).
+        constexpr int HROW = 1040;  // bytes per staged head row (1 KiB + 16: spreads heads over the banks)
+        constexpr int STAGE_OFF = 4096;
+        static_assert(2 * kWaves * X::BM * 4 <= STAGE_OFF && STAGE_OFF + X::BM * HROW <= X::RING, "staging fits");
 #pragma unroll
         for (int hb = 0; hb < HB; ++hb) {
             const int head = head0 + hb * 16 + en16;
             const float inv_l = 1.0f / l_run[hb];  // O and l share m_ref
-            uint16_t* orow = p.out + ((int64_t)c.token * p.H + head) * 512 + 128 * wave + 4 * eg;
+            const uint32_t srow = lds + STAGE_OFF + (uint32_t)((hb * 16 + en16) * HROW + 2 * (128 * wave + 4 * eg));
 #pragma unroll
-            for (int cb = 0; cb < 8; ++cb)
-                store_bf16x4(orow + 16 * cb, oacc[hb][cb][0] * inv_l, oacc[hb][cb][1] * inv_l, oacc[hb][cb][2] * inv_l,
-                             oacc[hb][cb][3] * inv_l);
+            for (int cb = 0; cb < 8; ++cb) {
+                bf16x4 v;
+                v[0] = (__bf16)(oacc[hb][cb][0] * inv_l);
+                v[1] = (__bf16)(oacc[hb][cb][1] * inv_l);
+                v[2] = (__bf16)(oacc[hb][cb][2] * inv_l);
+                v[3] = (__bf16)(oacc[hb][cb][3] * inv_l);
+                lds_store<bf16x4>(srow + 2 * 16 * cb, v);
+            }
             if (writes_ml) {
                 p.out_max[(int64_t)c.token * p.H + head] = m_true[hb] * kLn2;
                 p.out_sum[(int64_t)c.token * p.H + head] = l_run[hb] * fast_exp2(m_ref[hb] - m_true[hb]);
             }
         }
+        lds_barrier();
+        // wave w stores head rows w, w + 4, ...: 64 lanes x 16 bytes = one row
+        uint16_t* obase = p.out + ((int64_t)c.token * p.H + head0) * 512 + 8 * eln;
+#pragma unroll
+        for (int hr = wave; hr < X::BM; hr += kWaves)
+            *reinterpret_cast<bf16x8*>(obase + (int64_t)hr * 512) =
+                lds_load<bf16x8>(lds + STAGE_OFF + hr * HROW + 16 * eln);
     } else if (HB > 1 || p.arrivals == nullptr) {
 #pragma unroll
         for (int hb = 0; hb < HB; ++hb) {
