@@ -24,6 +24,7 @@ ROPE_DIM = 64
 FP8_ROW = 656  # bytes of an fp8 kv row: 512 e4m3 latent values, 4 fp32 scales, 64 bf16 rope values
 SCALE = 1.0 / 24.0  # 576 ** -0.5, the reference's fixed scale (README.md:81-83 of the reference)
 _LDS_BYTES = 2 * 64 * 1152 + 2048 * 4
+_PP_LDS_BYTES = 4 * 32 * 1152 + 2048 * 4 + 2 * 64 * 64  # ring, index cache, two P buffers
 
 
 @dataclass(frozen=True)
@@ -149,9 +150,13 @@ def plan_call(shape, config=None, cores: int = 256, kv_fp8: bool = False, w_uv_d
             raise ValueError("fp8 kv rows need a narrow plan (mfma=16)")
     batch, queries, heads, _, _ = shape
     tokens = batch * queries
-    variant = "xp" if config.pv_cols == 128 else ("wide" if config.mfma == 32 else "narrow")
+    if config.pv_cols == 128:
+        variant = "pp" if config.bm == 128 else "xp"
+    else:
+        variant = "wide" if config.mfma == 32 else "narrow"
+    threads, lds = (512, _PP_LDS_BYTES) if variant == "pp" else (256, _LDS_BYTES)
     launches = [Launch(f"sparse_mla_fwd_{variant}_h{config.bm}_kw{config.kv_waves}_bn{config.bn}_s{config.stages}",
-                       tokens * config.split * (heads // config.bm), 256, _LDS_BYTES)]
+                       tokens * config.split * (heads // config.bm), threads, lds)]
     partials = None
     merged = False
     if config.split > 1:

@@ -117,7 +117,9 @@ int plan_impl(int B, int SQ, int H, int L, int TOPK, int num_cus, bool fp8, bool
     // The column-split PV variants (pv_cols 128) replace narrow<2,2> and
     // narrow<1,4> on bf16 rows: measured 2-15 % faster on every shape swept
     // (no row-wave exchange in the epilogue); fp8 rows are read by the
-    // narrow variants only.
+    // narrow variants only.  The ping-pong variant (128 heads, pv_cols 128)
+    // measured 8 % under wide<4,1> per tile on the 4096- and 32768-token
+    // prefills.
     struct Variant {
         int hpg, kvw, bn, stages, mfma, pv_cols;
         bool bf16, fp8;
@@ -131,6 +133,7 @@ int plan_impl(int B, int SQ, int H, int L, int TOPK, int num_cus, bool fp8, bool
         {16, 4, 64, 2, 16, 512, false, true, 2800.0, 10000.0},   // narrow<1,4>
         {32, 4, 64, 2, 16, 128, true, false, 3800.0, 6000.0},    // xp<2>: 32 heads, column-split PV
         {16, 4, 64, 2, 16, 128, true, false, 2700.0, 4000.0},    // xp<1>: 16 heads, column-split PV
+        {128, 1, 32, 4, 16, 128, true, false, 4000.0, 18000.0},  // ping-pong: 128 heads, eight waves
     };
     constexpr double kClockMHz = 2200.0, kPrologueCycles = 9000.0, kLaunchUs = 2.0;
     constexpr double kHbmBytesPerUs = 4.8e6, kCuBytesPerUs = 3.0e4;                // sustained gather rates

@@ -1689,6 +1689,335 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd_xp(FwdParams p) {
     }
 }
 
+// ============================================================== ping-pong
+// 128 heads per workgroup, 8 waves in two groups of four (wave w is in group
+// w / 4; waves w and w + 4 share a SIMD).  Group k owns heads 64k .. 64k+63.
+// Per tile a group runs
+//   QK + softmax: wave = 16 heads (Q in registers) x the tile's 32 rows; P
+//                 (bf16) goes to the group's LDS buffer,
+//   PV:           wave = the group's 64 heads x 128 of the 512 columns (O in
+//                 registers), P read back from LDS,
+// and the two groups run half a tile apart, so that on every SIMD one wave's
+// softmax (VALU) overlaps the other wave's MFMAs (a single wave's VALU and
+// MFMA instructions do not overlap):
+//   half 2t:   group 0 QK + softmax (t)    group 1 PV (t - 1)
+//   half 2t+1: group 0 PV (t)              group 1 QK + softmax (t)
+// with a workgroup barrier at the start of every half.  Split merge: the
+// two-launch path only (no in-kernel merge).
+constexpr int kPPWaves = 8;
+constexpr int kPPThreads = 64 * kPPWaves;
+#ifndef PP_QK_DEPTH
+#define PP_QK_DEPTH 6
+#endif
+
+struct PPLds {
+    static constexpr int BN = 32, NSTAGE = 4;
+    static constexpr int KV_BYTES = BN * 1024;
+    static constexpr int STAGE_BYTES = BN * 1152;
+    static constexpr int IDX_OFF = NSTAGE * STAGE_BYTES;
+    // P of one group: 64 heads x 32 bf16 in the k order of the PV B operand
+    // (position 8 g + j holds tile row 4 g + j for j < 4, 16 + 4 g + j - 4
+    // otherwise), 64 bytes per head.
+    static constexpr int P_OFF = IDX_OFF + DSA_IDX_CAP * 4;
+    static constexpr int P_GROUP = 64 * 64;
+    static constexpr int LDS_BYTES = P_OFF + 2 * P_GROUP;
+    // per group-0 wave and tile: 8 kv rows + 8 rope rows
+    static constexpr int LOADS_PER_TILE = 9;
+    static_assert(LDS_BYTES <= 160 * 1024, "LDS budget");
+    static_assert(DSA_IDX_CAP % 256 == 0, "index cache fetched by the first 256 threads");
+    __device__ static uint32_t stage(uint32_t lds, int t) { return lds + (uint32_t)(t % NSTAGE) * STAGE_BYTES; }
+};
+
+__device__ __forceinline__ void pp_issue(const FwdParams& p, const Gather& gt, int t, uint32_t stage,
+                                         uint32_t idx_lds, int gw, int lane) {
+    const int rows = p.kv_rows;
+    const int r0 = 8 * gw;
+    const int my_id = lds_load<int>(idx_lds + 4 * (t * PPLds::BN + r0 + (lane & 7)));
+    const uint32_t my_row = (uint32_t)min(max(my_id, 0), rows - 1);
+    const uint32_t lane16 = (uint32_t)lane << 4;
+#pragma unroll
+    for (int rr = 0; rr < 8; ++rr)
+        gather_row(stage + (r0 + rr) * 1024, row_rsrc(gt.kv, __builtin_amdgcn_readlane(my_row, rr)), lane16,
+                   (uint32_t)sw_kv(r0 + rr) << 4);
+    const int r = r0 + (lane >> 3);
+    const int id = lds_load<int>(idx_lds + 4 * (t * PPLds::BN + r));
+    const uint32_t voff = ((uint32_t)min(max(id, 0), rows - 1) << 7) + (((lane & 7) ^ sw_rope(r)) << 4);
+    gather_lanes(stage + PPLds::KV_BYTES + r0 * 128, gt.kr, voff);
+}
+
+__global__ __launch_bounds__(kPPThreads, 1) void sparse_mla_fwd_pp(FwdParams p) {
+    using X = PPLds;
+    constexpr int BN = X::BN;
+    __shared__ __attribute__((aligned(1024))) char smem[X::LDS_BYTES];
+    const uint32_t lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)smem;
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int grp = wave >> 2;  // 0: QK half-steps even, 1: odd
+    const int gw = wave & 3;    // QK: head block gw of the group; PV: columns 128 gw ..
+    const int g = lane >> 4;
+    const int n16 = lane & 15;
+
+    const WgCoords c = wg_coords<BN>(p);
+    const int ghead0 = c.hgi * 128 + 64 * grp;  // first head of the group
+    const uint32_t idx_lds = lds + X::IDX_OFF;
+    const uint32_t p_lds = lds + X::P_OFF + grp * X::P_GROUP;
+
+    // Index loads first (threads 0..255 fill the cache).
+    IdxRegs<> ids;
+    if (wave < 4) ids = fetch_indices<BN>(p, c);
+
+    // ---- Q fragments of the QK heads: lane holds Q[head][128 g + 8 ks .. + 7];
+    // ks 16, 17 from q_rope (dims 32 (ks - 16) + 8 g).
+    bf16x8 qf[18];
+    {
+        const int head = ghead0 + 16 * gw + n16;
+        const uint16_t* qrow = p.q + ((int64_t)c.token * p.H + head) * 512 + 128 * g;
+#pragma unroll
+        for (int ks = 0; ks < 16; ++ks) qf[ks] = *reinterpret_cast<const bf16x8*>(qrow + 8 * ks);
+        const uint16_t* rrow = p.q_rope + ((int64_t)c.token * p.H + head) * 64 + 8 * g;
+        qf[16] = *reinterpret_cast<const bf16x8*>(rrow);
+        qf[17] = *reinterpret_cast<const bf16x8*>(rrow + 32);
+    }
+    if (wave < 4) store_indices(ids, idx_lds);
+    lds_barrier();
+    const Gather gt = make_gather(p, c.b);
+
+    // ---- running state (log2 units) of the 16 QK heads, and O of the PV block
+    f32x4 oacc[4][8];  // [head block][column block]
+    float m_ref = -FLT_MAX, m_true = -FLT_MAX, l_run = 0.f;
+
+    // QK + softmax of tile t for this wave's 16 heads; P to the group buffer.
+    auto qk_softmax = [&](int t, bool& overflow) __attribute__((always_inline)) {
+        const uint32_t stage = X::stage(lds, t);
+        int ln = lane;
+        asm volatile("" : "+v"(ln));
+        const int lg = ln >> 4, ln16 = ln & 15;
+        // K fragment of k-step ks, subtile s: row 16 s + n16, logical chunk
+        // 16 g + ks (kv) at byte 256 g + ((ks ^ sw_kv(n16)) << 4); rope chunk
+        // 4 (ks - 16) + g at ((4 (ks - 16) + g) ^ sw_rope(n16)) << 4.  Rows are
+        // 1 KiB (kv) / 128 B (rope) aligned, so the XORs act on a per-lane base.
+        const uint32_t kbase = (stage + ln16 * 1024 + ((uint32_t)lg << 8)) | ((uint32_t)sw_kv(ln16) << 4);
+        const uint32_t rbase = (stage + X::KV_BYTES + ln16 * 128) | ((uint32_t)(lg ^ sw_rope(ln16)) << 4);
+        auto kfrag = [&](int step) -> bf16x8 {
+            const int ks = step >> 1, sub = step & 1;
+            if (ks < 16) return lds_load<bf16x8>((kbase ^ (16u * ks)) + sub * 16 * 1024);
+            return lds_load<bf16x8>((rbase ^ (64u * (ks - 16))) + sub * 16 * 128);
+        };
+        constexpr int KD = PP_QK_DEPTH;
+        // The chain is on the critical path of its half-step: it runs at a
+        // raised wave priority over the other group's PV.
+        __builtin_amdgcn_s_setprio(2);
+        f32x4 sacc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+        i32x4 ivs[2];  // slot indices of the lane's score rows, read late in the chain
+        bf16x8 kf[KD];
+#pragma unroll
+        for (int j = 0; j < KD; ++j) kf[j] = kfrag(j);
+#pragma unroll
+        for (int step = 0; step < 36; ++step) {
+            sacc[step & 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[step % KD], qf[step >> 1], sacc[step & 1], 0, 0, 0);
+            if (step + KD < 36) kf[step % KD] = kfrag(step + KD);
+            if (step == 30)
+#pragma unroll
+                for (int sub = 0; sub < 2; ++sub)
+                    ivs[sub] = lds_load<i32x4>(idx_lds + 4 * (t * BN + 16 * sub + 4 * lg));
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        __builtin_amdgcn_s_setprio(0);
+        // Lane holds rows 16 s + 4 g + r of head n16.  Raw scores with masked
+        // rows at -inf; the scale folds into the max and one FMA per score.
+        // When a head of the wave has grown past m_ref + kRestartLog2 the pass
+        // is to be discarded and a clamp keeps it free of inf.
+        float x[8];
+        float smax = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < 8; ++r) {
+            x[r] = ivs[r >> 2][r & 3] < 0 ? -INFINITY : sacc[r >> 2][r & 3];
+            smax = fmaxf(smax, x[r]);
+        }
+        smax = max_xor32(max_xor16(smax));
+        m_true = fmaxf(m_true, smax * p.score_scale_log2);
+        if (m_ref == -FLT_MAX) m_ref = m_true;  // first valid rows: O and l are still zero
+        const bool ovf = m_true > m_ref + kRestartLog2;
+        overflow |= ovf;
+        const bool capped = __any(ovf);
+        const float neg_ref = -m_ref;
+        float psum = 0.f;
+        bf16x8 pk;
+#pragma unroll
+        for (int r = 0; r < 8; ++r) {
+            const float a = fmaf(x[r], p.score_scale_log2, neg_ref);
+            const float e = fast_exp2(capped ? fminf(a, kRestartLog2) : a);
+            psum += e;
+            pk[r] = (__bf16)e;
+        }
+        l_run += psum;
+        lds_store<bf16x8>(p_lds + (16 * gw + ln16) * 64 + 16 * lg, pk);
+    };
+
+    // PV of tile t: O[head block hb][column block cb] += V^T . P^T over the
+    // tile's 32 rows (one 16x16x32 MFMA per block pair).
+    auto pv = [&](int t) __attribute__((always_inline)) {
+        const uint32_t stage = X::stage(lds, t);
+        int ln = lane;
+        asm volatile("" : "+v"(ln));
+        const int lg = ln >> 4, ln16 = ln & 15;
+        bf16x8 pf[4];
+#pragma unroll
+        for (int hb = 0; hb < 4; ++hb) pf[hb] = lds_load<bf16x8>(p_lds + (16 * hb + ln16) * 64 + 16 * lg);
+        // V^T fragment of column block cb (columns 128 gw + 16 cb ..): transposed
+        // reads of rows 4 g + n16/4 and 16 + 4 g + n16/4 at column 4 (n16 & 3):
+        // logical chunk 16 gw + 2 cb + ((n16 & 3) >> 1), byte 8 (n16 & 1); the
+        // row is 1 KiB aligned and (2 cb + c) ^ sw = 2 cb ^ (c ^ sw) for c < 2.
+        const int tr_row = 4 * lg + (ln16 >> 2);
+        const uint32_t vbase = (stage + tr_row * 1024 + ((uint32_t)gw << 8)) |
+                               ((uint32_t)((((ln16 & 3) >> 1) ^ sw_kv(tr_row)) << 4) + ((ln16 & 1) << 3));
+        auto vfrag = [&](int cb) -> bf16x8 {
+            const uint32_t a = vbase ^ (32u * cb);
+            const bf16x4 v0 = lds_load_tr(a);
+            const bf16x4 v1 = lds_load_tr(a + 16 * 1024);
+            return __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7);
+        };
+        bf16x8 vf[2];
+        vf[0] = vfrag(0);
+        vf[1] = vfrag(1);
+#pragma unroll
+        for (int cb = 0; cb < 8; ++cb) {
+#pragma unroll
+            for (int hb = 0; hb < 4; ++hb)
+                oacc[hb][cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf[cb & 1], pf[hb], oacc[hb][cb], 0, 0, 0);
+            if (cb + 2 < 8) vf[cb & 1] = vfrag(cb + 2);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+
+    // At most two passes over the range (see kRestartLog2), as in the wide variant.
+#pragma unroll 1
+    for (int pass = 0; pass < 2; ++pass) {
+#pragma unroll
+        for (int hb = 0; hb < 4; ++hb)
+#pragma unroll
+            for (int cb = 0; cb < 8; ++cb) oacc[hb][cb] = f32x4{0.f, 0.f, 0.f, 0.f};
+        l_run = 0.f;
+        if (pass == 1) m_ref = m_true;
+        bool overflow = false;
+        if (grp == 0)
+#pragma unroll
+            for (int i = 0; i < 3; ++i)
+                if (i < c.nt) pp_issue(p, gt, i, X::stage(lds, i), idx_lds, gw, lane);
+        // Q (and the first tiles) complete here; see the wide variant.
+        wait_vmcnt<0>();
+
+        // Half 2t starts when group 0's gathers of tile t have landed (tiles up
+        // to t + 2 issued) and every wave is past half 2t - 1; in half 2t + 1
+        // group 0 issues tile t + 3 into the stage of tile t - 1, whose last
+        // reader (group 1's PV) ran in half 2t.
+        if (grp == 0) {
+            for (int t = 0; t < c.nt; ++t) {
+                const int ahead = min(2, c.nt - 1 - t);
+                if (ahead >= 2) wait_vmcnt<2 * X::LOADS_PER_TILE>();
+                else if (ahead == 1) wait_vmcnt<X::LOADS_PER_TILE>();
+                else wait_vmcnt<0>();
+                lds_barrier();
+                qk_softmax(t, overflow);
+                lds_barrier();
+                if (t + 3 < c.nt) pp_issue(p, gt, t + 3, X::stage(lds, t + 3), idx_lds, gw, lane);
+                pv(t);
+            }
+            if (c.nt > 0) lds_barrier();  // half 2 nt: group 1's last PV
+        } else if (c.nt > 0) {
+            lds_barrier();
+            lds_barrier();
+            qk_softmax(0, overflow);
+            for (int t = 1; t < c.nt; ++t) {
+                lds_barrier();
+                pv(t - 1);
+                lds_barrier();
+                qk_softmax(t, overflow);
+            }
+            lds_barrier();
+            pv(c.nt - 1);
+        }
+        // ---- workgroup vote: does any head need pass 1?  (The flag lives in
+        // the P buffers, free once every wave is past its last PV.)
+        if (pass == 1) break;
+        const uint32_t flag_lds = lds + X::P_OFF;
+        lds_barrier();
+        if (threadIdx.x == 0) lds_store<int>(flag_lds, 0);
+        lds_barrier();
+        if (__any(overflow) && lane == 0) lds_store<int>(flag_lds, 1);
+        lds_barrier();
+        if (__builtin_amdgcn_readfirstlane(lds_load<int>(flag_lds)) == 0) break;
+    }
+
+    // ---- epilogue: the QK waves publish (l, m_ref, m_true) of their heads;
+    // the PV waves scale their blocks.  Staging lives in the ring (free).
+    lds_barrier();  // every wave is past its last ring and P read
+    const uint32_t ml = lds + X::IDX_OFF;  // [3][128] floats (index cache no longer needed)
+    l_run = sum_xor32(sum_xor16(l_run));
+    int eln = lane;
+    asm volatile("" : "+v"(eln));
+    const int eg = eln >> 4, en16 = eln & 15;
+    if (eg == 0) {
+        const int hl = 64 * grp + 16 * gw + en16;  // head within the workgroup
+        lds_store<float>(ml + 4 * hl, l_run);
+        lds_store<float>(ml + 4 * (128 + hl), m_ref);
+        lds_store<float>(ml + 4 * (256 + hl), m_true);
+    }
+    lds_barrier();
+    if (p.nsplit == 1) {
+        constexpr int HROW = 1040;  // bytes per staged head row (1 KiB + 16: spreads heads over the banks)
+        static_assert(128 * HROW <= X::IDX_OFF, "staged rows fit the ring");
+#pragma unroll
+        for (int hb = 0; hb < 4; ++hb) {
+            const int hl = 64 * grp + 16 * hb + en16;
+            const float l = lds_load<float>(ml + 4 * hl);
+            const float mr = lds_load<float>(ml + 4 * (128 + hl));
+            const float mt = lds_load<float>(ml + 4 * (256 + hl));
+            const float inv_l = 1.0f / l;  // O and l share m_ref
+            const uint32_t srow = lds + (uint32_t)(hl * HROW + 2 * (128 * gw + 4 * eg));
+#pragma unroll
+            for (int cb = 0; cb < 8; ++cb) {
+                bf16x4 v;
+                v[0] = (__bf16)(oacc[hb][cb][0] * inv_l);
+                v[1] = (__bf16)(oacc[hb][cb][1] * inv_l);
+                v[2] = (__bf16)(oacc[hb][cb][2] * inv_l);
+                v[3] = (__bf16)(oacc[hb][cb][3] * inv_l);
+                lds_store<bf16x4>(srow + 2 * 16 * cb, v);
+            }
+            if (gw == 0 && eg == 0) {
+                const int head = c.hgi * 128 + hl;
+                p.out_max[(int64_t)c.token * p.H + head] = mt * kLn2;
+                p.out_sum[(int64_t)c.token * p.H + head] = l * fast_exp2(mr - mt);
+            }
+        }
+        lds_barrier();
+        // wave w stores head rows w, w + 8, ...: 64 lanes x 16 bytes = one row
+        uint16_t* obase = p.out + ((int64_t)c.token * p.H + c.hgi * 128) * 512 + 8 * eln;
+#pragma unroll 4
+        for (int hr = wave; hr < 128; hr += kPPWaves)
+            *reinterpret_cast<bf16x8*>(obase + (int64_t)hr * 512) = lds_load<bf16x8>(lds + hr * HROW + 16 * eln);
+    } else {
+#pragma unroll
+        for (int hb = 0; hb < 4; ++hb) {
+            const int hl = 64 * grp + 16 * hb + en16;
+            const int head = c.hgi * 128 + hl;
+            const float l = lds_load<float>(ml + 4 * hl);
+            const float mr = lds_load<float>(ml + 4 * (128 + hl));
+            const float mt = lds_load<float>(ml + 4 * (256 + hl));
+            const float to_true = fast_exp2(mr - mt);
+            const int64_t prow = ((int64_t)c.token * p.nsplit + c.sp) * p.H + head;
+            float* orow = p.part_o + prow * 512 + 128 * gw + 4 * eg;
+#pragma unroll
+            for (int cb = 0; cb < 8; ++cb) *reinterpret_cast<f32x4*>(orow + 16 * cb) = oacc[hb][cb] * to_true;
+            if (gw == 0 && eg == 0) {
+                p.part_m[prow] = mt * kLn2;
+                p.part_l[prow] = l * to_true;
+            }
+        }
+    }
+}
+
 template <typename K>
 int launch(K kernel, const FwdParams& p, hipStream_t stream) {
     hipLaunchKernelGGL(kernel, dim3((unsigned)fwd_grid(p)), dim3(kThreads), 0, stream, p);
@@ -1698,6 +2027,8 @@ int launch(K kernel, const FwdParams& p, hipStream_t stream) {
 }  // namespace
 
 bool fwd_variant_exists(int hpg, int kvw, int bn, int stages, int mfma, int pv_cols) {
+    if (pv_cols == 128 && hpg == 128)  // ping-pong: eight waves, 32-row tiles in a 4-stage ring
+        return mfma == 16 && kvw == 1 && bn == 32 && stages == 4;
     if (pv_cols == 128)  // column-split PV: four waves, 64-row tiles, 16, 32 or 64 heads
         return mfma == 16 && kvw == 4 && bn == 64 && stages == 2 && (hpg == 16 || hpg == 32 || hpg == 64);
     if (pv_cols != 512) return false;
@@ -1719,6 +2050,10 @@ int launch_fwd(const FwdParams& p, int hpg, int kvw, int bn, int stages, int mfm
     if (!fwd_variant_exists(hpg, kvw, bn, stages, mfma, pv_cols)) return (int)hipErrorInvalidValue;
     if (p.kv_fp8 && (mfma != 16 || pv_cols != 512)) return (int)hipErrorInvalidValue;  // fp8 rows: narrow variants only
     if (pv_cols == 128) {
+        if (hpg == 128) {
+            hipLaunchKernelGGL(sparse_mla_fwd_pp, dim3((unsigned)fwd_grid(p)), dim3(kPPThreads), 0, stream, p);
+            return (int)hipGetLastError();
+        }
         if (hpg == 16) return launch(sparse_mla_fwd_xp<1>, p, stream);
         if (hpg == 32) return launch(sparse_mla_fwd_xp<2>, p, stream);
         return launch(sparse_mla_fwd_xp<4>, p, stream);

@@ -127,7 +127,11 @@ PLANS_H128 = [Tuning(128, 32, 1, stages=4), Tuning(128, 32, 3, stages=4), Tuning
               # column-split PV (pv_cols 128): 16, 32 and 64 heads per group
               Tuning(16, 64, 1, kv_waves=4, mfma=16, pv_cols=128), Tuning(16, 64, 9, kv_waves=4, mfma=16, pv_cols=128),
               Tuning(32, 64, 1, kv_waves=4, mfma=16, pv_cols=128), Tuning(32, 64, 5, kv_waves=4, mfma=16, pv_cols=128),
-              Tuning(64, 64, 2, kv_waves=4, mfma=16, pv_cols=128), Tuning(64, 64, 7, kv_waves=4, mfma=16, pv_cols=128)]
+              Tuning(64, 64, 2, kv_waves=4, mfma=16, pv_cols=128), Tuning(64, 64, 7, kv_waves=4, mfma=16, pv_cols=128),
+              # ping-pong (128 heads, eight waves): one tile, three and 64 splits
+              Tuning(128, 32, 1, kv_waves=1, stages=4, mfma=16, pv_cols=128),
+              Tuning(128, 32, 3, kv_waves=1, stages=4, mfma=16, pv_cols=128),
+              Tuning(128, 32, 64, kv_waves=1, stages=4, mfma=16, pv_cols=128)]
 
 
 @pytest.mark.parametrize("config", PLANS_H128, ids=str)
@@ -191,6 +195,33 @@ def _random_case(seed, B, SQ, H, L, K, invalid=0.1, dup=0.1):
 def test_edge_shapes(B, SQ, H, L, K):
     data = _random_case(B * 1000 + K, B, SQ, H, L, K)
     _run_and_check(f"edge-{B}x{SQ}x{H}x{L}x{K}", data)
+
+
+_PP = dict(kv_waves=1, stages=4, mfma=16, pv_cols=128)
+
+
+@pytest.mark.parametrize("B,SQ,H,L,K,split", [
+    (1, 1, 128, 1, 1, 1),          # one row, one slot
+    (1, 3, 128, 5, 70, 1),         # TOPK > L: heavy duplication, ragged last tile
+    (1, 3, 128, 5, 70, 3),         # ... one tile per split
+    (1, 2, 128, 3000, 2047, 1),    # ragged by one
+    (1, 2, 128, 3000, 2047, 5),
+    (2, 1, 256, 20000, 4096, 2),   # two head groups, TOPK 4096 (index cache forces split >= 2)
+    (2, 1, 256, 20000, 4096, 7),
+])
+def test_ping_pong_edge_shapes(B, SQ, H, L, K, split):
+    data = _random_case(B * 1000 + K + split, B, SQ, H, L, K)
+    _run_and_check(f"pp-edge-{B}x{SQ}x{H}x{L}x{K}-s{split}", data, config=Tuning(128, 32, split, **_PP))
+
+
+def test_ping_pong_deterministic_bitwise():
+    data = _random_case(13, 1, 64, 128, 32768, 2048)
+    cfg = Tuning(128, 32, 1, **_PP)
+    a = dsa_amd.forward(*data, config=cfg)
+    b = dsa_amd.forward(*data, config=cfg)
+    torch.cuda.synchronize()
+    for x, y in zip(a, b):
+        assert torch.equal(x, y)
 
 
 def test_all_slots_twice_doubles_sum():

@@ -105,6 +105,9 @@ def test_plan_call_allocations_and_launches():
     assert launches[0].grid == 8 * config.split * (128 // config.bm)
     config, partials, launches = plan_call(CASE_SHAPES["c5_prefill_h128"], cores=256)
     assert config.split == 1 and partials is None and len(launches) == 1
+    # 128 heads, column-split PV: the eight-wave ping-pong kernel
+    assert launches[0].name.startswith("sparse_mla_fwd_pp") and launches[0].block == 512
+    assert launches[0].lds_bytes == 160 * 1024
 
 
 def test_plan_call_fused_merge_is_one_launch():
