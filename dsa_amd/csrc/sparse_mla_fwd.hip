@@ -1826,8 +1826,6 @@ __global__ __launch_bounds__(kPPThreads, 1) void sparse_mla_fwd_pp(FwdParams p) 
         __builtin_amdgcn_s_setprio(0);
         // Lane holds rows 16 s + 4 g + r of head n16.  Raw scores with masked
         // rows at -inf; the scale folds into the max and one FMA per score.
-        // When a head of the wave has grown past m_ref + kRestartLog2 the pass
-        // is to be discarded and a clamp keeps it free of inf.
         float x[8];
         float smax = -INFINITY;
 #pragma unroll
@@ -1840,16 +1838,23 @@ __global__ __launch_bounds__(kPPThreads, 1) void sparse_mla_fwd_pp(FwdParams p) 
         if (m_ref == -FLT_MAX) m_ref = m_true;  // first valid rows: O and l are still zero
         const bool ovf = m_true > m_ref + kRestartLog2;
         overflow |= ovf;
-        const bool capped = __any(ovf);
         const float neg_ref = -m_ref;
         float psum = 0.f;
         bf16x8 pk;
+        if (__any(ovf)) {  // this pass is to be discarded: the clamp keeps it free of inf
 #pragma unroll
-        for (int r = 0; r < 8; ++r) {
-            const float a = fmaf(x[r], p.score_scale_log2, neg_ref);
-            const float e = fast_exp2(capped ? fminf(a, kRestartLog2) : a);
-            psum += e;
-            pk[r] = (__bf16)e;
+            for (int r = 0; r < 8; ++r) {
+                const float e = fast_exp2(fminf(fmaf(x[r], p.score_scale_log2, neg_ref), kRestartLog2));
+                psum += e;
+                pk[r] = (__bf16)e;
+            }
+        } else {  // every P <= 2^kRestartLog2
+#pragma unroll
+            for (int r = 0; r < 8; ++r) {
+                const float e = fast_exp2(fmaf(x[r], p.score_scale_log2, neg_ref));
+                psum += e;
+                pk[r] = (__bf16)e;
+            }
         }
         l_run += psum;
         lds_store<bf16x8>(p_lds + (16 * gw + ln16) * 64 + 16 * lg, pk);
