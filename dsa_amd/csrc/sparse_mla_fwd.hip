@@ -1717,7 +1717,8 @@ struct PPLds {
     static constexpr int IDX_OFF = NSTAGE * STAGE_BYTES;
     // P of one group: 64 heads x 32 bf16 in the k order of the PV B operand
     // (position 8 g + j holds tile row 4 g + j for j < 4, 16 + 4 g + j - 4
-    // otherwise), 64 bytes per head.
+    // otherwise), 64 bytes per head; the 16-byte chunk of k-group g of head h
+    // sits at pp_pchunk(h, g).
     static constexpr int P_OFF = IDX_OFF + DSA_IDX_CAP * 4;
     static constexpr int P_GROUP = 64 * 64;
     static constexpr int LDS_BYTES = P_OFF + 2 * P_GROUP;
@@ -1728,6 +1729,19 @@ struct PPLds {
     __device__ static uint32_t stage(uint32_t lds, int t) { return lds + (uint32_t)(t % NSTAGE) * STAGE_BYTES; }
 };
 
+// Byte offset of k-group g's 16-byte P chunk of head h (within a 64-head
+// buffer).  With 64-byte heads, the lanes of one ds_read_b128 / ds_write_b128
+// pass (four quads of a half-wave, chosen by popcount parity) would meet 4
+// heads apart on the same banks; XOR-ing the chunk with f(h / 4) =
+// {0, 2, 3, 1} gives every pass 16 distinct bank groups.
+__device__ __forceinline__ uint32_t pp_pchunk(int h, int g) {
+    return (uint32_t)(h * 64 + 16 * (g ^ ((0x78 >> (2 * ((h >> 2) & 3))) & 3)));
+}
+
+// Gather of tile t, by the four waves of group 0 (gw = wave 0..3): kv rows
+// 8 gw .. 8 gw + 7 (one instruction per row) and rope rows 8 gw .. 8 gw + 7
+// (one instruction).  Group 1 issues nothing: the gathers are issued in the
+// half-steps in which group 0 runs PV, off the critical QK path.
 __device__ __forceinline__ void pp_issue(const FwdParams& p, const Gather& gt, int t, uint32_t stage,
                                          uint32_t idx_lds, int gw, int lane) {
     const int rows = p.kv_rows;
@@ -1857,7 +1871,7 @@ __global__ __launch_bounds__(kPPThreads, 1) void sparse_mla_fwd_pp(FwdParams p) 
             }
         }
         l_run += psum;
-        lds_store<bf16x8>(p_lds + (16 * gw + ln16) * 64 + 16 * lg, pk);
+        lds_store<bf16x8>(p_lds + pp_pchunk(16 * gw + ln16, lg), pk);
     };
 
     // PV of tile t: O[head block hb][column block cb] += V^T . P^T over the
@@ -1869,7 +1883,7 @@ __global__ __launch_bounds__(kPPThreads, 1) void sparse_mla_fwd_pp(FwdParams p) 
         const int lg = ln >> 4, ln16 = ln & 15;
         bf16x8 pf[4];
 #pragma unroll
-        for (int hb = 0; hb < 4; ++hb) pf[hb] = lds_load<bf16x8>(p_lds + (16 * hb + ln16) * 64 + 16 * lg);
+        for (int hb = 0; hb < 4; ++hb) pf[hb] = lds_load<bf16x8>(p_lds + pp_pchunk(16 * hb + ln16, lg));
         // V^T fragment of column block cb (columns 128 gw + 16 cb ..): transposed
         // reads of rows 4 g + n16/4 and 16 + 4 g + n16/4 at column 4 (n16 & 3):
         // logical chunk 16 gw + 2 cb + ((n16 & 3) >> 1), byte 8 (n16 & 1); the
