@@ -16,8 +16,10 @@ from oracle import dsa_oracle as O
 
 pytestmark = pytest.mark.gpu
 
+_PP = dict(kv_waves=1, stages=4, mfma=16, pv_cols=128)
 PLANS = [None, Tuning(128, 32, 1, stages=4), Tuning(128, 32, 3, stages=4), Tuning(64, 64, 2, kv_waves=2),
-         Tuning(32, 64, 1, kv_waves=2, mfma=16), Tuning(16, 64, 3, kv_waves=4, mfma=16)]
+         Tuning(32, 64, 1, kv_waves=2, mfma=16), Tuning(16, 64, 3, kv_waves=4, mfma=16),
+         Tuning(128, 32, 1, **_PP), Tuning(128, 32, 3, **_PP)]
 
 
 @pytest.fixture(scope="module", autouse=True)
@@ -70,7 +72,7 @@ def _check(tag, out, mx, sm, ref):
 
 
 @pytest.mark.parametrize("scale", [192 ** -0.5, 0.03, 1.0 / 24.0])
-@pytest.mark.parametrize("config", [None, Tuning(32, 64, 1, kv_waves=2, mfma=16)], ids=str)
+@pytest.mark.parametrize("config", [None, Tuning(32, 64, 1, kv_waves=2, mfma=16), Tuning(128, 32, 2, **_PP)], ids=str)
 def test_scale_parity(scale, config):
     data = _case(1)
     print(f"[scale {scale:.5f} {config}] launching", flush=True)
@@ -118,7 +120,8 @@ def test_paged_holes_are_masked(config):
 FAR_ENTRIES = [2 ** 25 + 1, 2 ** 26 + 1, 2 ** 31 - 1, -(2 ** 31), -2]
 
 
-@pytest.mark.parametrize("config", [None, Tuning(128, 32, 1, stages=4), Tuning(16, 64, 3, kv_waves=4, mfma=16)],
+@pytest.mark.parametrize("config", [None, Tuning(128, 32, 1, stages=4), Tuning(16, 64, 3, kv_waves=4, mfma=16),
+                                    Tuning(128, 32, 1, **_PP)],
                          ids=str)
 def test_paged_far_block_entries_are_masked(config):
     q, kv, qr, kr, ids = _case(8)

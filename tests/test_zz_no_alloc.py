@@ -105,6 +105,8 @@ CASES = [
     (((16, 2, 16, 8192, 2048), (5, 2, 16, 4096, 2000)), Tuning(16, 64, 2, kv_waves=4, mfma=16, fused_merge=True)),
     (((4, 2, 64, 8192, 2048), (2, 1, 64, 4096, 700)), Tuning(64, 64, 4, kv_waves=2)),               # wide, split 4
     (((2, 40, 128, 8192, 2048), (1, 7, 128, 2048, 512)), Tuning(128, 32, 1, stages=4)),              # no split
+    (((2, 16, 128, 8192, 2048), (1, 5, 128, 4096, 700)),
+     Tuning(128, 32, 2, kv_waves=1, stages=4, mfma=16, pv_cols=128)),                                # ping-pong, split 2
 ]
 
 
