@@ -155,6 +155,8 @@ def plan_call(shape, config=None, cores: int = 256, kv_fp8: bool = False, w_uv_d
     else:
         variant = "wide" if config.mfma == 32 else "narrow"
     threads, lds = (512, _PP_LDS_BYTES) if variant == "pp" else (256, _LDS_BYTES)
+    if variant == "xp" and config.bm == 16:
+        threads = 512  # four compute waves and four gather waves
     launches = [Launch(f"sparse_mla_fwd_{variant}_h{config.bm}_kw{config.kv_waves}_bn{config.bn}_s{config.stages}",
                        tokens * config.split * (heads // config.bm), threads, lds)]
     partials = None

@@ -1353,6 +1353,15 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd_narrow(FwdParams p
 // columns.  The four waves share one reference max per head, fixed from the
 // first tile with a valid row (the restart logic of the other variants applies
 // unchanged to it).
+//
+// PROD adds four gather waves (waves 4..7, one per SIMD beside a compute
+// wave): a wave stalls while the texture path accepts its row loads (≈0.7 us
+// per 64-row tile at ≈50 B/clk per CU), and with separate gather waves that
+// stall no longer holds up the compute waves' MFMAs.  The gather waves pass
+// every workgroup barrier the compute waves pass (they mirror the
+// reference-max exchange from the same LDS values) and hold no accumulators.
+// The 16-head kernel fits 2 waves per SIMD (252 VGPRs, no spills); the 32-
+// and 64-head kernels do not and run without gather waves.
 template <int HB>
 struct XpLds {
     static constexpr int BM = 16 * HB;
@@ -1371,8 +1380,8 @@ struct XpLds {
     static_assert(2 * kWaves * BM * 4 <= RING, "epilogue exchange fits the ring");
 };
 
-template <int HB>
-__global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd_xp(FwdParams p) {
+template <int HB, bool PROD>
+__global__ __launch_bounds__(PROD ? 2 * kThreads : kThreads, 1) void sparse_mla_fwd_xp(FwdParams p) {
     using R = Ring<64, 2>;
     using X = XpLds<HB>;
     constexpr int kBN = 64;
@@ -1381,18 +1390,23 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd_xp(FwdParams p) {
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    // With PROD, waves 4..7 only gather (wave 4 + w fetches what wave w
+    // would) and keep the workgroup barriers in step with the compute waves.
+    const bool producer = PROD && wave >= kWaves;
+    const int gw = producer ? wave - kWaves : wave;
     const int g = lane >> 4;
     const int n16 = lane & 15;
 
     const WgCoords c = wg_coords<kBN>(p);
     const int head0 = c.hgi * X::BM;
-    const IdxRegs<X::IDX_CAP> ids = fetch_indices<kBN, X::IDX_CAP>(p, c);
+    IdxRegs<X::IDX_CAP> ids;
+    if (!producer) ids = fetch_indices<kBN, X::IDX_CAP>(p, c);
 
     // ---- Q fragments of the HB head blocks (as in the narrow variant):
     // lane holds Q[head][128 g + 8 ks .. + 7]; ks 16, 17 from q_rope.
     bf16x8 qf[HB][18];
 #pragma unroll
-    for (int hb = 0; hb < HB; ++hb) {
+    for (int hb = 0; hb < (producer ? 0 : HB); ++hb) {
         const int head = head0 + hb * 16 + n16;
         const uint16_t* qrow = p.q + ((int64_t)c.token * p.H + head) * 512 + 128 * g;
 #pragma unroll
@@ -1403,7 +1417,7 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd_xp(FwdParams p) {
     }
 
     const uint32_t idx_lds = lds + X::IDX_OFF;
-    store_indices(ids, idx_lds);
+    if (!producer) store_indices(ids, idx_lds);
     lds_barrier();
     const Gather gt = make_gather(p, c.b);
 
@@ -1446,13 +1460,27 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd_xp(FwdParams p) {
         }
         bool ref_set = pass == 1;  // pass 1 runs against the exact max (set at the vote)
         bool overflow = false;
-        issue_tile<R>(p, gt, 0, R::stage(lds, 0), idx_lds, wave, lane);
+        if (!PROD || producer) issue_tile<R>(p, gt, 0, R::stage(lds, 0), idx_lds, gw, lane);
         wait_vmcnt<0>();  // Q and tile 0
 
         for (int t = 0; t < c.nt; ++t) {
             if (t > 0) wait_vmcnt<0>();  // this wave's gathers of tile t
             lds_barrier();                // tile t complete; stage of tile t - 1, P and MX free
-            if (t + 1 < c.nt) issue_tile<R>(p, gt, t + 1, R::stage(lds, t + 1), idx_lds, wave, lane);
+            if (t + 1 < c.nt && (!PROD || producer))
+                issue_tile<R>(p, gt, t + 1, R::stage(lds, t + 1), idx_lds, gw, lane);
+            if (producer) {
+                // The compute waves' barriers of this tile: the reference max
+                // exchange (same decision, from the same LDS values) and P.
+                if (!ref_set) {
+                    lds_barrier();
+                    float t0 = -INFINITY;
+#pragma unroll
+                    for (int w = 0; w < kWaves; ++w) t0 = fmaxf(t0, lds_load<float>(mx_lds + 4 * (w * X::BM)));
+                    if (__builtin_amdgcn_readfirstlane(__float_as_int(t0)) != __float_as_int(-INFINITY)) ref_set = true;
+                }
+                lds_barrier();
+                continue;
+            }
             const uint32_t stage = R::stage(lds, t);
 
             // ---- S^T = K . Q^T for this wave's 16 rows and HB head blocks.
@@ -1581,7 +1609,7 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd_xp(FwdParams p) {
         lds_barrier();
         if (__builtin_amdgcn_readfirstlane(lds_load<int>(flag_lds)) == 0) break;
         // pass 1 runs against the exact max over all waves
-        if (g == 0)
+        if (g == 0 && !producer)
 #pragma unroll
             for (int hb = 0; hb < HB; ++hb) lds_store<float>(mx_lds + 4 * (wave * X::BM + hb * 16 + n16), m_true[hb]);
         lds_barrier();
@@ -1598,6 +1626,17 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd_xp(FwdParams p) {
     // ---- epilogue: sum l and take the max over the four waves' rows (the ring
     // is free once every wave is past its last read).
     lds_barrier();
+    if (producer) {
+        // the compute waves' remaining barriers
+        lds_barrier();
+        if (p.nsplit == 1) {
+            lds_barrier();
+        } else if (!(HB > 1 || p.arrivals == nullptr)) {
+            lds_barrier();
+            lds_barrier();
+        }
+        return;
+    }
     const uint32_t l_lds = lds, mt_lds = lds + kWaves * X::BM * 4;
 #pragma unroll
     for (int hb = 0; hb < HB; ++hb) {
@@ -2038,8 +2077,8 @@ __global__ __launch_bounds__(kPPThreads, 1) void sparse_mla_fwd_pp(FwdParams p) 
 }
 
 template <typename K>
-int launch(K kernel, const FwdParams& p, hipStream_t stream) {
-    hipLaunchKernelGGL(kernel, dim3((unsigned)fwd_grid(p)), dim3(kThreads), 0, stream, p);
+int launch(K kernel, const FwdParams& p, hipStream_t stream, int threads = kThreads) {
+    hipLaunchKernelGGL(kernel, dim3((unsigned)fwd_grid(p)), dim3(threads), 0, stream, p);
     return (int)hipGetLastError();
 }
 
@@ -2073,9 +2112,9 @@ int launch_fwd(const FwdParams& p, int hpg, int kvw, int bn, int stages, int mfm
             hipLaunchKernelGGL(sparse_mla_fwd_pp, dim3((unsigned)fwd_grid(p)), dim3(kPPThreads), 0, stream, p);
             return (int)hipGetLastError();
         }
-        if (hpg == 16) return launch(sparse_mla_fwd_xp<1>, p, stream);
-        if (hpg == 32) return launch(sparse_mla_fwd_xp<2>, p, stream);
-        return launch(sparse_mla_fwd_xp<4>, p, stream);
+        if (hpg == 16) return launch(sparse_mla_fwd_xp<1, true>, p, stream, 2 * kThreads);
+        if (hpg == 32) return launch(sparse_mla_fwd_xp<2, false>, p, stream);
+        return launch(sparse_mla_fwd_xp<4, false>, p, stream);
     }
     if (mfma == 32) {
         if (hpg == 128) return launch(sparse_mla_fwd_wide<4, 1, 32, 4>, p, stream);

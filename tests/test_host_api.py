@@ -103,6 +103,8 @@ def test_plan_call_allocations_and_launches():
     assert partials == ((8, 1, config.split, 128, 512), (8, 1, config.split, 128))
     assert [l.name for l in launches] == [launches[0].name, "merge_partials"]
     assert launches[0].grid == 8 * config.split * (128 // config.bm)
+    # 16 heads, column-split PV: four compute waves and four gather waves
+    assert launches[0].name.startswith("sparse_mla_fwd_xp_h16") and launches[0].block == 512
     config, partials, launches = plan_call(CASE_SHAPES["c5_prefill_h128"], cores=256)
     assert config.split == 1 and partials is None and len(launches) == 1
     # 128 heads, column-split PV: the eight-wave ping-pong kernel
