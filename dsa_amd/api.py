@@ -27,6 +27,11 @@ _LDS_BYTES = 2 * 64 * 1152 + 2048 * 4
 _PP_LDS_BYTES = 4 * 32 * 1152 + 2048 * 4 + 2 * 64 * 64  # ring, index cache, two P buffers
 
 
+def _xs_lds_bytes(bm):
+    # ring, index cache, two P buffers, (l, reference max, max) per head, vote flag
+    return 4 * 32 * 1152 + 2048 * 4 + 2 * bm * 64 + 3 * bm * 4 + 16
+
+
 @dataclass(frozen=True)
 class Launch:
     """Descriptor of one kernel launch of a call (``return_kernels=True``)."""
@@ -151,12 +156,14 @@ def plan_call(shape, config=None, cores: int = 256, kv_fp8: bool = False, w_uv_d
     batch, queries, heads, _, _ = shape
     tokens = batch * queries
     if config.pv_cols == 128:
-        variant = "pp" if config.bm == 128 else "xp"
+        variant = "pp" if config.bm == 128 else "xs" if config.bn == 32 else "xp"
     else:
         variant = "wide" if config.mfma == 32 else "narrow"
     threads, lds = (512, _PP_LDS_BYTES) if variant == "pp" else (256, _LDS_BYTES)
     if variant == "xp" and config.bm == 16:
         threads = 512  # four compute waves and four gather waves
+    if variant == "xs":  # QK waves (one per 16 heads), two PV waves, four gather waves
+        threads, lds = 64 * (config.bm // 16 + 6), _xs_lds_bytes(config.bm)
     launches = [Launch(f"sparse_mla_fwd_{variant}_h{config.bm}_kw{config.kv_waves}_bn{config.bn}_s{config.stages}",
                        tokens * config.split * (heads // config.bm), threads, lds)]
     partials = None

@@ -133,15 +133,20 @@ _XP32 = dict(kv_waves=4, mfma=16, pv_cols=128)
 # by 8 % on the two large 128-head prefills; on decode-sized shapes the
 # column-split and narrow plans stay 20 % to 4x ahead.
 _PP = dict(kv_waves=1, stages=4, mfma=16, pv_cols=128)
+# Specialised waves (16 or 32 heads, 32-row tiles, four gather waves holding
+# three tiles in registers): ahead by 4-9 % on the 8- and 32-token decodes
+# (input sets cycled beyond the MALL) and the 16- and 128-query prefills
+# with 32 heads per group.
+_XS = dict(kv_waves=2, stages=4, mfma=16, pv_cols=128)
 SELECTED = {
     "decode_b1": Tuning(16, 64, 16, **_XP16),
-    "decode_b8": Tuning(16, 64, 4, **_XP16),
-    "decode_b32": Tuning(64, 64, 4, kv_waves=1, mfma=16),
+    "decode_b8": Tuning(32, 32, 8, **_XS),
+    "decode_b32": Tuning(32, 32, 2, **_XS),
     "decode_tp8": Tuning(16, 64, 16, **_XP16),
-    "prefill_q16": Tuning(32, 64, 4, **_XP32),
+    "prefill_q16": Tuning(32, 32, 4, **_XS),
     "prefill_q64": Tuning(32, 64, 1, **_XP32),
     "prefill_tp8": Tuning(16, 64, 2, fused_merge=True, **_XP16),
-    "prefill_k512": Tuning(32, 64, 1, **_XP32),
+    "prefill_k512": Tuning(32, 32, 1, **_XS),
     "decode_b4_h128": Tuning(16, 64, 8, **_XP16),
     "prefill_b4_h128": Tuning(128, 32, 1, **_PP),
     "decode_b4_h64": Tuning(16, 64, 16, **_XP16),
@@ -151,7 +156,7 @@ SELECTED = {
     "decode_b4_h16": Tuning(16, 64, 32, **_XP16),
     "prefill_b4_h16": Tuning(16, 64, 1, **_XP16),
     "c1_decode_b1": Tuning(16, 64, 16, **_XP16),
-    "c2_decode_b8": Tuning(16, 64, 4, **_XP16),
+    "c2_decode_b8": Tuning(32, 32, 8, **_XS),
     "c3_decode_h16_mtp": Tuning(16, 64, 2, fused_merge=True, **_XP16),
     "c4_prefill_h16": Tuning(16, 64, 1, **_XP16),
     "c5_prefill_h128": Tuning(128, 32, 1, **_PP),

@@ -81,11 +81,11 @@ int dsa_plan_check(const dsa_plan* plan, int B, int SQ, int H, int L, int TOPK) 
         return fail(-1, "split %d leaves more than %d slots per workgroup (TOPK=%d)", split, cap, TOPK);
     if (plan->fused_merge != 0 && plan->fused_merge != 1)
         return fail(-1, "fused_merge must be 0 or 1 (got %d)", plan->fused_merge);
-    if (plan->fused_merge && (mfma != 16 || split > kMaxFusedSplit || (pv_cols == 128 && hpg != 16)))
+    if (plan->fused_merge && (mfma != 16 || split > kMaxFusedSplit || (pv_cols == 128 && (hpg != 16 || bn != 64))))
         return fail(-1,
-                    "fused_merge needs a narrow plan (mfma 16; with pv_cols 128, 16 heads per group) with split <= %d "
-                    "(got mfma=%d split=%d heads_per_group=%d pv_cols=%d)",
-                    kMaxFusedSplit, mfma, split, hpg, pv_cols);
+                    "fused_merge needs a narrow plan (mfma 16; with pv_cols 128, 16 heads per group and tile_rows 64) "
+                    "with split <= %d (got mfma=%d split=%d heads_per_group=%d tile_rows=%d pv_cols=%d)",
+                    kMaxFusedSplit, mfma, split, hpg, bn, pv_cols);
     g_err[0] = 0;
     return 0;
 }
@@ -119,7 +119,9 @@ int plan_impl(int B, int SQ, int H, int L, int TOPK, int num_cus, bool fp8, bool
     // (no row-wave exchange in the epilogue); fp8 rows are read by the
     // narrow variants only.  The ping-pong variant (128 heads, pv_cols 128)
     // measured 8 % under wide<4,1> per tile on the 4096- and 32768-token
-    // prefills.
+    // prefills.  The specialised-wave variants (32-row tiles, gather waves)
+    // measured within ±9 % of the column-split ones, ahead where a workgroup
+    // holds 32 heads.
     struct Variant {
         int hpg, kvw, bn, stages, mfma, pv_cols;
         bool bf16, fp8;
@@ -134,6 +136,8 @@ int plan_impl(int B, int SQ, int H, int L, int TOPK, int num_cus, bool fp8, bool
         {32, 4, 64, 2, 16, 128, true, false, 3800.0, 6000.0},    // xp<2>: 32 heads, column-split PV
         {16, 4, 64, 2, 16, 128, true, false, 2700.0, 4000.0},    // xp<1>: 16 heads, column-split PV
         {128, 1, 32, 4, 16, 128, true, false, 4000.0, 18000.0},  // ping-pong: 128 heads, eight waves
+        {32, 2, 32, 4, 16, 128, true, false, 1850.0, 6000.0},    // xs<2>: 32 heads, specialised waves
+        {16, 2, 32, 4, 16, 128, true, false, 1400.0, 4000.0},    // xs<1>: 16 heads, specialised waves
     };
     constexpr double kClockMHz = 2200.0, kPrologueCycles = 9000.0, kLaunchUs = 2.0;
     constexpr double kHbmBytesPerUs = 4.8e6, kCuBytesPerUs = 3.0e4;                // sustained gather rates
@@ -174,7 +178,7 @@ int plan_impl(int B, int SQ, int H, int L, int TOPK, int num_cus, bool fp8, bool
             }
             double cost = kLaunchUs + main_us + merge_us;
             int fused = 0;
-            if (fuse && split > 1 && split <= kMaxFusedSplit && v.mfma == 16) {
+            if (fuse && split > 1 && split <= kMaxFusedSplit && v.mfma == 16 && !(v.pv_cols == 128 && v.bn == 32)) {
                 const double group_bytes = (double)split * v.hpg * 2056.0;
                 const double fused_cost = kLaunchUs + main_us + kFusedUs + group_bytes / kFusedBytesPerUs;
                 if (fused_cost < cost) cost = fused_cost, fused = 1;

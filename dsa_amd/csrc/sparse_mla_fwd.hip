@@ -1728,6 +1728,392 @@ __global__ __launch_bounds__(PROD ? 2 * kThreads : kThreads, 1) void sparse_mla_
     }
 }
 
+// Byte offset of k-group g's 16-byte P chunk of head h (within a 64-head
+// buffer).  With 64-byte heads, the lanes of one ds_read_b128 / ds_write_b128
+// pass (four quads of a half-wave, chosen by popcount parity) would meet 4
+// heads apart on the same banks; XOR-ing the chunk with f(h / 4) =
+// {0, 2, 3, 1} gives every pass 16 distinct bank groups.
+__device__ __forceinline__ uint32_t pp_pchunk(int h, int g) {
+    return (uint32_t)(h * 64 + 16 * (g ^ ((0x78 >> (2 * ((h >> 2) & 3))) & 3)));
+}
+
+// ====================================================== specialised waves
+// 16 or 32 heads per workgroup (HB head blocks of 16), 32-row tiles in a
+// 4-stage ring, and waves with fixed roles (wave w runs on SIMD w % 4):
+//   waves 0 .. HB-1      QK + softmax: wave hb scores the tile's 32 rows
+//                        against head block hb (Q in registers) and writes
+//                        its bf16 P into P buffer s % 2;
+//   waves HB, HB+1       PV: wave v accumulates O for columns 256 v ..
+//                        256 v + 255 of all HB head blocks over tile s - 1
+//                        (one 16x16x32 MFMA per 16-column block and head
+//                        block);
+//   waves HB+2 .. HB+5   gathers: gather wave j loads kv rows 8 j .. 8 j + 7
+//                        of a tile and their rope rows into registers
+//                        (ordinary buffer loads, three tiles ahead) and writes
+//                        tile s + 2 into its ring stage during step s.
+// Steps s = 0 .. nt are separated by one workgroup barrier each.  A wave
+// stalls while the texture path accepts its loads; here only the gather
+// waves stall, and with three tiles of rows in their registers the load
+// latency hides behind the steps in between.  Tile t occupies stage t % 4
+// from step t - 2 (written) to step t + 1 (its PV); P(t) is written in step t
+// and read in step t + 1.  A QK wave owns every row of its 16 heads, so its
+// reference max is its own (set at its first valid rows, as in the ping-pong
+// kernel) and the restart logic applies unchanged.  Split merge: the
+// two-launch path only.
+// One QK or PV wave alone keeps a tile's LDS reads in flight, so its fragment
+// pipelines are deep (LDS latency under the gather writes is a few hundred
+// cycles; 14 reads of a wave may be outstanding).
+#ifndef XS_QK_DEPTH
+#define XS_QK_DEPTH 12
+#endif
+#ifndef XS_PV_DEPTH
+#define XS_PV_DEPTH 6
+#endif
+template <int HB>
+struct XsLds {
+    static constexpr int BN = 32, NSTAGE = 4;
+    static constexpr int KV_BYTES = BN * 1024;
+    static constexpr int STAGE_BYTES = BN * 1152;
+    static constexpr int IDX_OFF = NSTAGE * STAGE_BYTES;
+    // P of one tile: 16 HB heads x 32 bf16 in the k order of the PV B operand
+    // (position 8 g + j holds tile row 4 g + j for j < 4, 16 + 4 g + j - 4
+    // otherwise), 64 bytes per head; the 16-byte chunk of k-group g of head h
+    // sits at pp_pchunk(h, g).
+    static constexpr int P_OFF = IDX_OFF + DSA_IDX_CAP * 4;
+    static constexpr int P_BYTES = 16 * HB * 64;
+    static constexpr int EPI_OFF = P_OFF + 2 * P_BYTES;  // l, reference max, max: [3][16 HB] floats
+    static constexpr int FLAG_OFF = EPI_OFF + 3 * 16 * HB * 4;
+    static constexpr int LDS_BYTES = FLAG_OFF + 16;
+    static constexpr int WAVES = HB + 6;
+    static constexpr int DEPTH = 3;  // tiles held in the gather waves' registers
+    static_assert(LDS_BYTES <= 160 * 1024, "LDS budget");
+    __device__ static uint32_t stage(uint32_t lds, int t) { return lds + (uint32_t)(t % NSTAGE) * STAGE_BYTES; }
+};
+
+// One gather wave's share of a tile in registers: kv rows 8 j .. 8 j + 7
+// (lane l holds bytes (16 l) ^ (16 sw_kv(row)) of each) and one 16-byte chunk
+// of rope rows 8 j + l / 8.
+struct XsRows {
+    u32x4 v[9];
+};
+
+// Loads of tile t.  Tiles past the range load nothing (an empty descriptor:
+// the loads still issue, so the compiler's wait counts stay exact) and read
+// the index cache of the last tile.
+__device__ __forceinline__ void xs_load(const FwdParams& p, const char* kv, const char* kr, int t, int nt,
+                                        uint32_t idx_lds, int j, int lane, XsRows& b) {
+    const bool live = t < nt;
+    const int tt = max(min(t, nt - 1), 0);
+    const int rows = p.kv_rows;
+    const int r0 = 8 * j;
+    const int my_id = lds_load<int>(idx_lds + 4 * (tt * 32 + r0 + (lane & 7)));
+    const uint32_t my_row = (uint32_t)min(max(my_id, 0), rows - 1);
+    const uint32_t lane16 = (uint32_t)lane << 4;
+    const int row_bytes = live ? 1024 : 0;
+#pragma unroll
+    for (int rr = 0; rr < 8; ++rr) {
+        const uint32_t row = __builtin_amdgcn_readlane(my_row, rr);
+        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<char*>(kv) + ((uint64_t)row << 10), (short)0, row_bytes, 0x00020000);
+        b.v[rr] = __builtin_amdgcn_raw_buffer_load_b128(rs, lane16 ^ ((uint32_t)sw_kv(r0 + rr) << 4), 0, 0);
+    }
+    const int r = r0 + (lane >> 3);
+    const int id = lds_load<int>(idx_lds + 4 * (tt * 32 + r));
+    const uint32_t voff = ((uint32_t)min(max(id, 0), rows - 1) << 7) + (((lane & 7) ^ sw_rope(r)) << 4);
+    const __amdgpu_buffer_rsrc_t rr = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(kr), (short)0,
+                                                                        live ? rows * 128 : 0, 0x00020000);
+    b.v[8] = __builtin_amdgcn_raw_buffer_load_b128(rr, voff, 0, 0);
+    __builtin_amdgcn_sched_barrier(0);  // keep the issue order: the loads of later tiles stay in flight
+}
+// The same rows into the stage of tile t (the layout the LDS-DMA gathers of
+// the other variants produce).
+__device__ __forceinline__ void xs_store(uint32_t stage, int j, int lane, const XsRows& b) {
+    const uint32_t st = stage + ((uint32_t)lane << 4);
+#pragma unroll
+    for (int rr = 0; rr < 8; ++rr) lds_store<u32x4>(st + (8 * j + rr) * 1024, b.v[rr]);
+    lds_store<u32x4>(st + 32 * 1024 + 8 * j * 128, b.v[8]);
+    __builtin_amdgcn_sched_barrier(0);
+}
+
+template <int HB>
+__global__ __launch_bounds__(64 * XsLds<HB>::WAVES, 1) void sparse_mla_fwd_xs(FwdParams p) {
+    using X = XsLds<HB>;
+    constexpr int BN = X::BN;
+    constexpr int BM = 16 * HB;
+    __shared__ __attribute__((aligned(1024))) char smem[X::LDS_BYTES];
+    const uint32_t lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)smem;
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int g = lane >> 4;
+    const int n16 = lane & 15;
+
+    const WgCoords c = wg_coords<BN>(p);
+    const int head0 = c.hgi * BM;
+    const uint32_t idx_lds = lds + X::IDX_OFF;
+    const uint32_t p_lds = lds + X::P_OFF;
+    const uint32_t epi = lds + X::EPI_OFF;
+    const uint32_t flag_lds = lds + X::FLAG_OFF;
+
+    // Index loads (threads 0..255: QK, PV and the first gather waves).
+    IdxRegs<> ids;
+    if (wave < 4) ids = fetch_indices<BN>(p, c);
+    // Q of the QK wave's head block: lane holds Q[head][128 g + 8 ks .. + 7];
+    // ks 16, 17 from q_rope (dims 32 (ks - 16) + 8 g).
+    bf16x8 qf[18];
+    if (wave < HB) {
+        const int head = head0 + 16 * wave + n16;
+        const uint16_t* qrow = p.q + ((int64_t)c.token * p.H + head) * 512 + 128 * g;
+#pragma unroll
+        for (int ks = 0; ks < 16; ++ks) qf[ks] = *reinterpret_cast<const bf16x8*>(qrow + 8 * ks);
+        const uint16_t* rrow = p.q_rope + ((int64_t)c.token * p.H + head) * 64 + 8 * g;
+        qf[16] = *reinterpret_cast<const bf16x8*>(rrow);
+        qf[17] = *reinterpret_cast<const bf16x8*>(rrow + 32);
+    }
+    if (wave < 4) store_indices(ids, idx_lds);
+    lds_barrier();
+
+    // Second-pass vote (every wave): the flag is raised by a QK wave whose
+    // scores outgrew its reference max by more than kRestartLog2.
+    auto vote = [&](bool overflow) -> bool {
+        if (threadIdx.x == 0) lds_store<int>(flag_lds, 0);
+        lds_barrier();
+        if (__any(overflow) && lane == 0) lds_store<int>(flag_lds, 1);
+        lds_barrier();
+        return __builtin_amdgcn_readfirstlane(lds_load<int>(flag_lds)) != 0;
+    };
+    // End of every wave, after the PV waves' epilogue (split 1): the output
+    // rows staged by the PV waves; wave w stores head rows w, w + WAVES, ...:
+    // 64 lanes x 16 bytes = one row.
+    auto finish = [&]() {
+        if (p.nsplit != 1) return;
+        lds_barrier();  // rows staged
+        uint16_t* obase = p.out + ((int64_t)c.token * p.H + head0) * 512 + 8 * lane;
+        for (int hr = wave; hr < BM; hr += X::WAVES)
+            *reinterpret_cast<bf16x8*>(obase + (int64_t)hr * 512) = lds_load<bf16x8>(lds + hr * 1040 + 16 * lane);
+    };
+
+    if (wave >= HB + 2) {
+        // ---- gather waves
+        const int j = wave - (HB + 2);
+        const int64_t first = p.block_table ? 0 : (int64_t)c.b * p.L;  // first row of the addressed range
+        const char* kv = reinterpret_cast<const char*>(p.kv) + first * 1024;
+        const char* kr = reinterpret_cast<const char*>(p.k_rope) + first * 128;
+        XsRows rb[X::DEPTH];
+#pragma unroll 1
+        for (int pass = 0; pass < 2; ++pass) {
+#pragma unroll
+            for (int i = 0; i < X::DEPTH; ++i) xs_load(p, kv, kr, i, c.nt, idx_lds, j, lane, rb[i]);
+            xs_store(X::stage(lds, 0), j, lane, rb[0]);
+            xs_load(p, kv, kr, X::DEPTH, c.nt, idx_lds, j, lane, rb[0]);
+            xs_store(X::stage(lds, 1), j, lane, rb[1]);
+            xs_load(p, kv, kr, X::DEPTH + 1, c.nt, idx_lds, j, lane, rb[1]);
+            // Step s: tile s + 2 out of registers into its stage (free since
+            // the PV of tile s - 2 in step s - 1), tile s + 5 into the freed
+            // registers.  Steps 0 .. nt run in groups of DEPTH (static register
+            // indices) with the last partial group outside the loop: an exit
+            // inside the loop body would make the compiler's wait counts at
+            // the loop head conservative (vmcnt(0) before every store).
+            auto step = [&](int s, XsRows& b) __attribute__((always_inline)) {
+                lds_barrier();
+                xs_store(X::stage(lds, s + 2), j, lane, b);
+                xs_load(p, kv, kr, s + 2 + X::DEPTH, c.nt, idx_lds, j, lane, b);
+            };
+            static_assert(X::DEPTH == 3, "the step groups below assume three register tiles");
+            int s0 = 0;
+            for (; s0 + 2 <= c.nt; s0 += 3) {
+                step(s0, rb[2]);
+                step(s0 + 1, rb[0]);
+                step(s0 + 2, rb[1]);
+            }
+            if (s0 <= c.nt) step(s0, rb[2]);
+            if (s0 + 1 <= c.nt) step(s0 + 1, rb[0]);
+            if (pass == 1 || !vote(false)) break;
+        }
+        wait_vmcnt<0>();  // the loads past the range
+        lds_barrier();    // every wave past its last ring and P read
+        lds_barrier();    // l and the maxima published
+        finish();
+        return;
+    }
+
+    if (wave < HB) {
+        // ---- QK waves: S^T = K . Q^T for the tile's two 16-row subtiles.
+        const int hb = wave;
+        float m_ref = -FLT_MAX, m_true = -FLT_MAX, l_run = 0.f;
+#pragma unroll 1
+        for (int pass = 0; pass < 2; ++pass) {
+            l_run = 0.f;
+            if (pass == 1) m_ref = m_true;  // pass 1 runs against the exact max
+            bool overflow = false;
+            for (int s = 0; s <= c.nt; ++s) {
+                lds_barrier();
+                if (s == c.nt) break;
+                const uint32_t stage = X::stage(lds, s);
+                // K fragment of k-step ks, subtile sub: row 16 sub + n16, logical
+                // chunk 16 g + ks (kv) at byte 256 g + ((ks ^ sw_kv(n16)) << 4);
+                // rope chunk 4 (ks - 16) + g at ((4 (ks - 16) + g) ^ sw_rope(n16)) << 4.
+                const uint32_t kbase = (stage + n16 * 1024 + ((uint32_t)g << 8)) | ((uint32_t)sw_kv(n16) << 4);
+                const uint32_t rbase = (stage + X::KV_BYTES + n16 * 128) | ((uint32_t)(g ^ sw_rope(n16)) << 4);
+                auto kfrag = [&](int st) -> bf16x8 {
+                    const int ks = st >> 1, sub = st & 1;
+                    if (ks < 16) return lds_load<bf16x8>((kbase ^ (16u * ks)) + sub * 16 * 1024);
+                    return lds_load<bf16x8>((rbase ^ (64u * (ks - 16))) + sub * 16 * 128);
+                };
+                constexpr int KD = XS_QK_DEPTH;
+                f32x4 sacc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+                i32x4 ivs[2];
+                bf16x8 kf[KD];
+#pragma unroll
+                for (int jj = 0; jj < KD; ++jj) kf[jj] = kfrag(jj);
+#pragma unroll
+                for (int st = 0; st < 36; ++st) {
+                    sacc[st & 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[st % KD], qf[st >> 1], sacc[st & 1], 0, 0, 0);
+                    if (st + KD < 36) kf[st % KD] = kfrag(st + KD);
+                    if (st == 30)
+#pragma unroll
+                        for (int sub = 0; sub < 2; ++sub)
+                            ivs[sub] = lds_load<i32x4>(idx_lds + 4 * (s * BN + 16 * sub + 4 * g));
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+                // Lane holds rows 16 sub + 4 g + r of head n16.  Raw scores with
+                // masked rows at -inf; the scale folds into the max and one FMA.
+                float x[8];
+                float smax = -INFINITY;
+#pragma unroll
+                for (int r = 0; r < 8; ++r) {
+                    x[r] = ivs[r >> 2][r & 3] < 0 ? -INFINITY : sacc[r >> 2][r & 3];
+                    smax = fmaxf(smax, x[r]);
+                }
+                smax = max_xor32(max_xor16(smax));
+                m_true = fmaxf(m_true, smax * p.score_scale_log2);
+                if (m_ref == -FLT_MAX) m_ref = m_true;  // first valid rows: O and l are still zero
+                const bool ovf = m_true > m_ref + kRestartLog2;
+                overflow |= ovf;
+                const float neg_ref = -m_ref;
+                float psum = 0.f;
+                bf16x8 pk;
+                if (__any(ovf)) {  // this pass is to be discarded: the clamp keeps it free of inf
+#pragma unroll
+                    for (int r = 0; r < 8; ++r) {
+                        const float e = fast_exp2(fminf(fmaf(x[r], p.score_scale_log2, neg_ref), kRestartLog2));
+                        psum += e;
+                        pk[r] = (__bf16)e;
+                    }
+                } else {  // every P <= 2^kRestartLog2
+#pragma unroll
+                    for (int r = 0; r < 8; ++r) {
+                        const float e = fast_exp2(fmaf(x[r], p.score_scale_log2, neg_ref));
+                        psum += e;
+                        pk[r] = (__bf16)e;
+                    }
+                }
+                l_run += psum;
+                lds_store<bf16x8>(p_lds + (uint32_t)(s & 1) * X::P_BYTES + pp_pchunk(16 * hb + n16, g), pk);
+            }
+            if (pass == 1 || !vote(overflow)) break;
+        }
+        lds_barrier();  // every wave past its last ring and P read
+        l_run = sum_xor32(sum_xor16(l_run));
+        if (g == 0) {
+            lds_store<float>(epi + 4 * (16 * hb + n16), l_run);
+            lds_store<float>(epi + 4 * (BM + 16 * hb + n16), m_ref);
+            lds_store<float>(epi + 4 * (2 * BM + 16 * hb + n16), m_true);
+        }
+        lds_barrier();  // l and the maxima published
+        finish();
+        return;
+    }
+
+    // ---- PV waves: O^T[columns 256 v ..][heads] += V^T . P^T over each tile's 32 rows
+    const int v = wave - HB;
+    f32x4 oacc[HB][16];
+    // V^T fragment of column block cb: transposed reads of rows 4 g + n16 / 4
+    // and 16 + 4 g + n16 / 4 at column 4 (n16 & 3) of the block, i.e. logical
+    // chunk 32 v + 2 cb + ((n16 & 3) >> 1), byte 8 (n16 & 1); the row is 1 KiB
+    // aligned and (2 cb + c) ^ sw = 2 cb ^ (c ^ sw) for c < 2.
+    const int tr_row = 4 * g + (n16 >> 2);
+    const uint32_t v_row = (uint32_t)tr_row * 1024 + ((uint32_t)v << 9);
+    const uint32_t v_sw = (uint32_t)(((((n16 & 3) >> 1) ^ sw_kv(tr_row)) << 4) + ((n16 & 1) << 3));
+#pragma unroll 1
+    for (int pass = 0; pass < 2; ++pass) {
+#pragma unroll
+        for (int hb = 0; hb < HB; ++hb)
+#pragma unroll
+            for (int cb = 0; cb < 16; ++cb) oacc[hb][cb] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int s = 0; s <= c.nt; ++s) {
+            lds_barrier();
+            if (s == 0) continue;
+            const int t = s - 1;
+            const uint32_t vbase = (X::stage(lds, t) + v_row) | v_sw;
+            bf16x8 pf[HB];
+#pragma unroll
+            for (int hb = 0; hb < HB; ++hb)
+                pf[hb] = lds_load<bf16x8>(p_lds + (uint32_t)(t & 1) * X::P_BYTES + pp_pchunk(16 * hb + n16, g));
+            auto vfrag = [&](int cb) -> bf16x8 {
+                const uint32_t a = vbase ^ (32u * cb);
+                const bf16x4 v0 = lds_load_tr(a);
+                const bf16x4 v1 = lds_load_tr(a + 16 * 1024);
+                return __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7);
+            };
+            constexpr int PV_DEPTH = XS_PV_DEPTH;
+            bf16x8 vf[PV_DEPTH];
+#pragma unroll
+            for (int jj = 0; jj < PV_DEPTH; ++jj) vf[jj] = vfrag(jj);
+#pragma unroll
+            for (int cb = 0; cb < 16; ++cb) {
+#pragma unroll
+                for (int hb = 0; hb < HB; ++hb)
+                    oacc[hb][cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf[cb % PV_DEPTH], pf[hb], oacc[hb][cb], 0, 0, 0);
+                if (cb + PV_DEPTH < 16) vf[cb % PV_DEPTH] = vfrag(cb + PV_DEPTH);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+        if (pass == 1 || !vote(false)) break;
+    }
+    lds_barrier();  // every wave past its last ring and P read
+    lds_barrier();  // l and the maxima published
+    const bool writes_ml = v == 0 && g == 0;
+#pragma unroll
+    for (int hb = 0; hb < HB; ++hb) {
+        const int hl = 16 * hb + n16;
+        const float l = lds_load<float>(epi + 4 * hl);
+        const float mr = lds_load<float>(epi + 4 * (BM + hl));
+        const float mt = lds_load<float>(epi + 4 * (2 * BM + hl));
+        const int head = head0 + hl;
+        if (p.nsplit == 1) {
+            // bf16 rows staged in the ring (a lane holds 4 columns of each of
+            // 16 column blocks), stored one 1 KiB head row per instruction.
+            const float inv_l = 1.0f / l;  // O and l share m_ref
+            const uint32_t srow = lds + (uint32_t)(hl * 1040 + 2 * (256 * v + 4 * g));
+#pragma unroll
+            for (int cb = 0; cb < 16; ++cb) {
+                bf16x4 o;
+                o[0] = (__bf16)(oacc[hb][cb][0] * inv_l);
+                o[1] = (__bf16)(oacc[hb][cb][1] * inv_l);
+                o[2] = (__bf16)(oacc[hb][cb][2] * inv_l);
+                o[3] = (__bf16)(oacc[hb][cb][3] * inv_l);
+                lds_store<bf16x4>(srow + 32 * cb, o);
+            }
+            if (writes_ml) {
+                p.out_max[(int64_t)c.token * p.H + head] = mt * kLn2;
+                p.out_sum[(int64_t)c.token * p.H + head] = l * fast_exp2(mr - mt);
+            }
+        } else {
+            const float to_true = fast_exp2(mr - mt);
+            const int64_t prow = ((int64_t)c.token * p.nsplit + c.sp) * p.H + head;
+            float* orow = p.part_o + prow * 512 + 256 * v + 4 * g;
+#pragma unroll
+            for (int cb = 0; cb < 16; ++cb) *reinterpret_cast<f32x4*>(orow + 16 * cb) = oacc[hb][cb] * to_true;
+            if (writes_ml) {
+                p.part_m[prow] = mt * kLn2;
+                p.part_l[prow] = l * to_true;
+            }
+        }
+    }
+    finish();
+}
+
 // ============================================================== ping-pong
 // 128 heads per workgroup, 8 waves in two groups of four (wave w is in group
 // w / 4; waves w and w + 4 share a SIMD).  Group k owns heads 64k .. 64k+63.
@@ -1768,14 +2154,6 @@ struct PPLds {
     __device__ static uint32_t stage(uint32_t lds, int t) { return lds + (uint32_t)(t % NSTAGE) * STAGE_BYTES; }
 };
 
-// Byte offset of k-group g's 16-byte P chunk of head h (within a 64-head
-// buffer).  With 64-byte heads, the lanes of one ds_read_b128 / ds_write_b128
-// pass (four quads of a half-wave, chosen by popcount parity) would meet 4
-// heads apart on the same banks; XOR-ing the chunk with f(h / 4) =
-// {0, 2, 3, 1} gives every pass 16 distinct bank groups.
-__device__ __forceinline__ uint32_t pp_pchunk(int h, int g) {
-    return (uint32_t)(h * 64 + 16 * (g ^ ((0x78 >> (2 * ((h >> 2) & 3))) & 3)));
-}
 
 // Gather of tile t, by the four waves of group 0 (gw = wave 0..3): kv rows
 // 8 gw .. 8 gw + 7 (one instruction per row) and rope rows 8 gw .. 8 gw + 7
@@ -2082,11 +2460,14 @@ int launch(K kernel, const FwdParams& p, hipStream_t stream, int threads = kThre
     return (int)hipGetLastError();
 }
 
+
 }  // namespace
 
 bool fwd_variant_exists(int hpg, int kvw, int bn, int stages, int mfma, int pv_cols) {
     if (pv_cols == 128 && hpg == 128)  // ping-pong: eight waves, 32-row tiles in a 4-stage ring
         return mfma == 16 && kvw == 1 && bn == 32 && stages == 4;
+    if (pv_cols == 128 && (hpg == 16 || hpg == 32) && bn == 32)  // specialised waves: 32-row tiles, 4 stages
+        return mfma == 16 && kvw == 2 && stages == 4;
     if (pv_cols == 128)  // column-split PV: four waves, 64-row tiles, 16, 32 or 64 heads
         return mfma == 16 && kvw == 4 && bn == 64 && stages == 2 && (hpg == 16 || hpg == 32 || hpg == 64);
     if (pv_cols != 512) return false;
@@ -2112,6 +2493,8 @@ int launch_fwd(const FwdParams& p, int hpg, int kvw, int bn, int stages, int mfm
             hipLaunchKernelGGL(sparse_mla_fwd_pp, dim3((unsigned)fwd_grid(p)), dim3(kPPThreads), 0, stream, p);
             return (int)hipGetLastError();
         }
+        if (hpg == 16 && bn == 32) return launch(sparse_mla_fwd_xs<1>, p, stream, 64 * XsLds<1>::WAVES);
+        if (hpg == 32 && bn == 32) return launch(sparse_mla_fwd_xs<2>, p, stream, 64 * XsLds<2>::WAVES);
         if (hpg == 16) return launch(sparse_mla_fwd_xp<1, true>, p, stream, 2 * kThreads);
         if (hpg == 32) return launch(sparse_mla_fwd_xp<2, false>, p, stream);
         return launch(sparse_mla_fwd_xp<4, false>, p, stream);

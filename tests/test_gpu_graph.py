@@ -41,6 +41,7 @@ CASES = [  # (B, SQ, H), plan, W_UV value dim (0: none)
     ((1, 40, 128), Tuning(128, 32, 1, stages=4), 0),                              # wide kernel, no split
     ((1, 40, 128), Tuning(128, 32, 1, kv_waves=1, stages=4, mfma=16, pv_cols=128), 0),   # ping-pong, no split
     ((2, 2, 128), Tuning(128, 32, 3, kv_waves=1, stages=4, mfma=16, pv_cols=128), 0),    # ping-pong + merge kernel
+    ((8, 1, 128), Tuning(32, 32, 8, kv_waves=2, stages=4, mfma=16, pv_cols=128), 0),     # specialised waves + merge
     ((2, 1, 128), Tuning(32, 64, 4, kv_waves=2, mfma=16), 128),                   # main + merge_uv
     ((2, 3, 16), Tuning(16, 64, 1, kv_waves=4, mfma=16), 128),                    # main + project_uv
 ]

@@ -19,7 +19,9 @@ pytestmark = pytest.mark.gpu
 _PP = dict(kv_waves=1, stages=4, mfma=16, pv_cols=128)
 PLANS = [None, Tuning(128, 32, 1, stages=4), Tuning(128, 32, 3, stages=4), Tuning(64, 64, 2, kv_waves=2),
          Tuning(32, 64, 1, kv_waves=2, mfma=16), Tuning(16, 64, 3, kv_waves=4, mfma=16),
-         Tuning(128, 32, 1, **_PP), Tuning(128, 32, 3, **_PP)]
+         Tuning(128, 32, 1, **_PP), Tuning(128, 32, 3, **_PP),
+         Tuning(16, 32, 2, kv_waves=2, stages=4, mfma=16, pv_cols=128),
+         Tuning(32, 32, 1, kv_waves=2, stages=4, mfma=16, pv_cols=128)]
 
 
 @pytest.fixture(scope="module", autouse=True)
@@ -72,7 +74,8 @@ def _check(tag, out, mx, sm, ref):
 
 
 @pytest.mark.parametrize("scale", [192 ** -0.5, 0.03, 1.0 / 24.0])
-@pytest.mark.parametrize("config", [None, Tuning(32, 64, 1, kv_waves=2, mfma=16), Tuning(128, 32, 2, **_PP)], ids=str)
+@pytest.mark.parametrize("config", [None, Tuning(32, 64, 1, kv_waves=2, mfma=16), Tuning(128, 32, 2, **_PP),
+                                    Tuning(16, 32, 3, kv_waves=2, stages=4, mfma=16, pv_cols=128)], ids=str)
 def test_scale_parity(scale, config):
     data = _case(1)
     print(f"[scale {scale:.5f} {config}] launching", flush=True)
@@ -121,7 +124,8 @@ FAR_ENTRIES = [2 ** 25 + 1, 2 ** 26 + 1, 2 ** 31 - 1, -(2 ** 31), -2]
 
 
 @pytest.mark.parametrize("config", [None, Tuning(128, 32, 1, stages=4), Tuning(16, 64, 3, kv_waves=4, mfma=16),
-                                    Tuning(128, 32, 1, **_PP)],
+                                    Tuning(128, 32, 1, **_PP),
+                                    Tuning(32, 32, 2, kv_waves=2, stages=4, mfma=16, pv_cols=128)],
                          ids=str)
 def test_paged_far_block_entries_are_masked(config):
     q, kv, qr, kr, ids = _case(8)

@@ -131,7 +131,13 @@ PLANS_H128 = [Tuning(128, 32, 1, stages=4), Tuning(128, 32, 3, stages=4), Tuning
               # ping-pong (128 heads, eight waves): one tile, three and 64 splits
               Tuning(128, 32, 1, kv_waves=1, stages=4, mfma=16, pv_cols=128),
               Tuning(128, 32, 3, kv_waves=1, stages=4, mfma=16, pv_cols=128),
-              Tuning(128, 32, 64, kv_waves=1, stages=4, mfma=16, pv_cols=128)]
+              Tuning(128, 32, 64, kv_waves=1, stages=4, mfma=16, pv_cols=128),
+              # specialised waves (16 or 32 heads, 32-row tiles, gather waves)
+              Tuning(16, 32, 1, kv_waves=2, stages=4, mfma=16, pv_cols=128),
+              Tuning(16, 32, 7, kv_waves=2, stages=4, mfma=16, pv_cols=128),
+              Tuning(32, 32, 1, kv_waves=2, stages=4, mfma=16, pv_cols=128),
+              Tuning(32, 32, 8, kv_waves=2, stages=4, mfma=16, pv_cols=128),
+              Tuning(32, 32, 64, kv_waves=2, stages=4, mfma=16, pv_cols=128)]
 
 
 @pytest.mark.parametrize("config", PLANS_H128, ids=str)
@@ -212,6 +218,25 @@ _PP = dict(kv_waves=1, stages=4, mfma=16, pv_cols=128)
 def test_ping_pong_edge_shapes(B, SQ, H, L, K, split):
     data = _random_case(B * 1000 + K + split, B, SQ, H, L, K)
     _run_and_check(f"pp-edge-{B}x{SQ}x{H}x{L}x{K}-s{split}", data, config=Tuning(128, 32, split, **_PP))
+
+
+_XS = dict(kv_waves=2, stages=4, mfma=16, pv_cols=128)
+
+
+@pytest.mark.parametrize("B,SQ,H,L,K,bm,split", [
+    (1, 1, 16, 1, 1, 16, 1),          # one row, one slot: steps 0 and 1 only
+    (1, 3, 32, 5, 70, 32, 1),         # TOPK > L: heavy duplication, ragged last tile
+    (1, 3, 32, 5, 70, 32, 3),         # one tile per split
+    (1, 2, 16, 3000, 2047, 16, 1),    # ragged by one; 64 steps
+    (2, 1, 64, 3000, 100, 32, 2),     # two head groups, four tiles, two splits of two
+    (2, 2, 48, 3000, 200, 16, 2),     # three head groups, seven tiles
+    (2, 1, 64, 20000, 4096, 32, 5),   # TOPK 4096 (index cache forces split >= 2)
+])
+def test_specialised_waves_edge_shapes(B, SQ, H, L, K, bm, split):
+    # nt = 1 .. 64 tiles per workgroup: the gather waves' register pipeline
+    # (three tiles ahead) with the tail steps of every residue of nt mod 3
+    data = _random_case(B * 1000 + K + split + bm, B, SQ, H, L, K)
+    _run_and_check(f"xs-edge-{B}x{SQ}x{H}x{L}x{K}-h{bm}-s{split}", data, config=Tuning(bm, 32, split, **_XS))
 
 
 def test_ping_pong_deterministic_bitwise():

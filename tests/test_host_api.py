@@ -90,8 +90,13 @@ def test_planner_covers_any_shape(shape):
     assert 1 <= plan.split <= ntiles
     assert -(-ntiles // plan.split) * plan.bn <= 2048  # index cache of one workgroup
     assert shape[2] % plan.bm == 0
-    if plan.pv_cols == 128:  # column-split PV: four waves share every head block
+    if plan.pv_cols == 128 and plan.bn == 32 and plan.bm < 128:  # specialised waves: 16 or 32 heads
+        assert plan.kv_waves == 2 and plan.stages == 4 and plan.mfma == 16 and plan.bm in (16, 32)
+        assert not plan.fused_merge  # the merge kernel only
+    elif plan.pv_cols == 128 and plan.bm < 128:  # column-split PV: four waves share every head block
         assert plan.kv_waves == 4 and plan.mfma == 16 and plan.bm in (16, 32, 64)
+    elif plan.pv_cols == 128:  # ping-pong
+        assert plan.kv_waves == 1 and plan.stages == 4 and plan.mfma == 16 and plan.bn == 32
     else:
         assert plan.bm // plan.mfma * plan.kv_waves == 4
 
@@ -103,8 +108,15 @@ def test_plan_call_allocations_and_launches():
     assert partials == ((8, 1, config.split, 128, 512), (8, 1, config.split, 128))
     assert [l.name for l in launches] == [launches[0].name, "merge_partials"]
     assert launches[0].grid == 8 * config.split * (128 // config.bm)
+    # 32 heads, specialised waves: two QK, two PV and four gather waves
+    assert launches[0].name.startswith("sparse_mla_fwd_xs_h32") and launches[0].block == 512
+    assert launches[0].lds_bytes == 4 * 32 * 1152 + 2048 * 4 + 2 * 32 * 64 + 3 * 32 * 4 + 16
     # 16 heads, column-split PV: four compute waves and four gather waves
+    _, _, launches = plan_call(shape, config=Tuning(16, 64, 4, kv_waves=4, mfma=16, pv_cols=128), cores=256)
     assert launches[0].name.startswith("sparse_mla_fwd_xp_h16") and launches[0].block == 512
+    # 16 heads, specialised waves: one QK wave, two PV and four gather waves
+    _, _, launches = plan_call(shape, config=Tuning(16, 32, 4, kv_waves=2, stages=4, mfma=16, pv_cols=128), cores=256)
+    assert launches[0].name.startswith("sparse_mla_fwd_xs_h16") and launches[0].block == 448
     config, partials, launches = plan_call(CASE_SHAPES["c5_prefill_h128"], cores=256)
     assert config.split == 1 and partials is None and len(launches) == 1
     # 128 heads, column-split PV: the eight-wave ping-pong kernel
