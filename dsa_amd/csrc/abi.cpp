@@ -81,11 +81,11 @@ int dsa_plan_check(const dsa_plan* plan, int B, int SQ, int H, int L, int TOPK) 
         return fail(-1, "split %d leaves more than %d slots per workgroup (TOPK=%d)", split, cap, TOPK);
     if (plan->fused_merge != 0 && plan->fused_merge != 1)
         return fail(-1, "fused_merge must be 0 or 1 (got %d)", plan->fused_merge);
-    if (plan->fused_merge && (mfma != 16 || split > kMaxFusedSplit || (pv_cols == 128 && (hpg != 16 || bn != 64))))
+    if (plan->fused_merge && (mfma != 16 || split > kMaxFusedSplit || (pv_cols == 128 && hpg != 16)))
         return fail(-1,
-                    "fused_merge needs a narrow plan (mfma 16; with pv_cols 128, 16 heads per group and tile_rows 64) "
-                    "with split <= %d (got mfma=%d split=%d heads_per_group=%d tile_rows=%d pv_cols=%d)",
-                    kMaxFusedSplit, mfma, split, hpg, bn, pv_cols);
+                    "fused_merge needs a narrow plan (mfma 16; with pv_cols 128, 16 heads per group) with split <= %d "
+                    "(got mfma=%d split=%d heads_per_group=%d pv_cols=%d)",
+                    kMaxFusedSplit, mfma, split, hpg, pv_cols);
     g_err[0] = 0;
     return 0;
 }
@@ -178,7 +178,7 @@ int plan_impl(int B, int SQ, int H, int L, int TOPK, int num_cus, bool fp8, bool
             }
             double cost = kLaunchUs + main_us + merge_us;
             int fused = 0;
-            if (fuse && split > 1 && split <= kMaxFusedSplit && v.mfma == 16 && !(v.pv_cols == 128 && v.bn == 32)) {
+            if (fuse && split > 1 && split <= kMaxFusedSplit && v.mfma == 16 && !(v.pv_cols == 128 && v.hpg != 16)) {
                 const double group_bytes = (double)split * v.hpg * 2056.0;
                 const double fused_cost = kLaunchUs + main_us + kFusedUs + group_bytes / kFusedBytesPerUs;
                 if (fused_cost < cost) cost = fused_cost, fused = 1;

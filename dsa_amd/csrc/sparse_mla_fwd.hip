@@ -881,10 +881,10 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t group_block(const FwdParams& p
 
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 
-template <int NCB>
-__device__ __forceinline__ void merge_if_last(const FwdParams& p, const WgCoords& c, int head0, int heads, int hl,
-                                              int g, bool writes_ml, int cb_lo, uint32_t flag_lds) {
-    static_assert(NCB % 8 == 0, "column blocks per lane");
+// Count-in of a workgroup's partials (every wave calls it): true in the
+// workgroup that arrives last, which then owns the group's merge and has
+// zeroed the counter for the next call.
+__device__ __forceinline__ bool group_count_in(const FwdParams& p, const WgCoords& c, uint32_t flag_lds) {
     wait_vmcnt<0>();  // this wave's partial stores have completed ...
     lds_barrier();    // ... and every other wave's
     const int64_t group = (int64_t)c.token * p.hgroups + c.hgi;
@@ -894,9 +894,18 @@ __device__ __forceinline__ void merge_if_last(const FwdParams& p, const WgCoords
         lds_store<int>(flag_lds, before + 1 == (uint32_t)p.nsplit ? 1 : 0);
     }
     lds_barrier();
-    if (__builtin_amdgcn_readfirstlane(lds_load<int>(flag_lds)) == 0) return;
+    if (__builtin_amdgcn_readfirstlane(lds_load<int>(flag_lds)) == 0) return false;
     if (threadIdx.x == 0) __hip_atomic_store(p.arrivals + group, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return true;
+}
 
+// The merge of a group by its last workgroup: this lane's columns, SPR
+// splits' partials in flight per round trip (the sum runs over the splits in
+// ascending order whatever SPR is).
+template <int NCB, int SPR = 4>
+__device__ __forceinline__ void merge_group_cols(const FwdParams& p, const WgCoords& c, int head0, int heads, int hl,
+                                                 int g, bool writes_ml, int cb_lo) {
+    static_assert(NCB % 8 == 0, "column blocks per lane");
     const int S = p.nsplit;  // 2..16, checked on the host
     const int head = head0 + hl;
     const int64_t row0 = (int64_t)c.token * S * p.H + head;  // (m, l) of split s: row0 + s * H
@@ -928,11 +937,11 @@ __device__ __forceinline__ void merge_if_last(const FwdParams& p, const WgCoords
 #pragma unroll
         for (int i = 0; i < 8; ++i) acc[i] = merge_f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int s0 = 0; s0 < 16; s0 += 4) {
+        for (int s0 = 0; s0 < 16; s0 += SPR) {
             if (s0 < S) {
-                merge_f32x4 u[4][8];
+                merge_f32x4 u[SPR][8];
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
+                for (int j = 0; j < SPR; ++j) {
                     if (s0 + j < S) {
                         const __amdgpu_buffer_rsrc_t rs = group_block(p, c.token, s0 + j, head0, heads);
 #pragma unroll
@@ -943,7 +952,7 @@ __device__ __forceinline__ void merge_if_last(const FwdParams& p, const WgCoords
                     }
                 }
 #pragma unroll
-                for (int j = 0; j < 4; ++j)
+                for (int j = 0; j < SPR; ++j)
                     if (s0 + j < S)
 #pragma unroll
                         for (int i = 0; i < 8; ++i) merge_add_cols(w[s0 + j], u[j][i], acc[i]);
@@ -957,6 +966,12 @@ __device__ __forceinline__ void merge_if_last(const FwdParams& p, const WgCoords
         p.out_max[(int64_t)c.token * p.H + head] = m;
         p.out_sum[(int64_t)c.token * p.H + head] = l;
     }
+}
+
+template <int NCB>
+__device__ __forceinline__ void merge_if_last(const FwdParams& p, const WgCoords& c, int head0, int heads, int hl,
+                                              int g, bool writes_ml, int cb_lo, uint32_t flag_lds) {
+    if (group_count_in(p, c, flag_lds)) merge_group_cols<NCB>(p, c, head0, heads, hl, g, writes_ml, cb_lo);
 }
 
 template <int HW, int KW, bool FP8 = false>
@@ -1758,8 +1773,10 @@ __device__ __forceinline__ uint32_t pp_pchunk(int h, int g) {
 // from step t - 2 (written) to step t + 1 (its PV); P(t) is written in step t
 // and read in step t + 1.  A QK wave owns every row of its 16 heads, so its
 // reference max is its own (set at its first valid rows, as in the ping-pong
-// kernel) and the restart logic applies unchanged.  Split merge: the
-// two-launch path only.
+// kernel) and the restart logic applies unchanged.  Split merge: the merge
+// kernel, or for 16 heads (arrival counters given) in the workgroup of each
+// (token, head group) that stores its partials last, as the column-split
+// kernel does (merge_if_last).
 // One QK or PV wave alone keeps a tile's LDS reads in flight, so its fragment
 // pipelines are deep (LDS latency under the gather writes is a few hundred
 // cycles; 14 reads of a wave may be outstanding).
@@ -1882,15 +1899,22 @@ __global__ __launch_bounds__(64 * XsLds<HB>::WAVES, 1) void sparse_mla_fwd_xs(Fw
         lds_barrier();
         return __builtin_amdgcn_readfirstlane(lds_load<int>(flag_lds)) != 0;
     };
-    // End of every wave, after the PV waves' epilogue (split 1): the output
+    // End of every wave, after the PV waves' epilogue.  Split 1: the output
     // rows staged by the PV waves; wave w stores head rows w, w + WAVES, ...:
-    // 64 lanes x 16 bytes = one row.
-    auto finish = [&]() {
-        if (p.nsplit != 1) return;
-        lds_barrier();  // rows staged
-        uint16_t* obase = p.out + ((int64_t)c.token * p.H + head0) * 512 + 8 * lane;
-        for (int hr = wave; hr < BM; hr += X::WAVES)
-            *reinterpret_cast<bf16x8*>(obase + (int64_t)hr * 512) = lds_load<bf16x8>(lds + hr * 1040 + 16 * lane);
+    // 64 lanes x 16 bytes = one row.  In-kernel merge (16 heads): every wave
+    // counts in; true in the group's last workgroup, where the PV waves then
+    // merge their columns.
+    auto finish = [&]() -> bool {
+        if (p.nsplit == 1) {
+            lds_barrier();  // rows staged
+            uint16_t* obase = p.out + ((int64_t)c.token * p.H + head0) * 512 + 8 * lane;
+            for (int hr = wave; hr < BM; hr += X::WAVES)
+                *reinterpret_cast<bf16x8*>(obase + (int64_t)hr * 512) =
+                    lds_load<bf16x8>(lds + hr * 1040 + 16 * lane);
+            return false;
+        }
+        if (HB > 1 || p.arrivals == nullptr) return false;
+        return group_count_in(p, c, flag_lds);
     };
 
     if (wave >= HB + 2) {
@@ -2099,7 +2123,7 @@ __global__ __launch_bounds__(64 * XsLds<HB>::WAVES, 1) void sparse_mla_fwd_xs(Fw
                 p.out_max[(int64_t)c.token * p.H + head] = mt * kLn2;
                 p.out_sum[(int64_t)c.token * p.H + head] = l * fast_exp2(mr - mt);
             }
-        } else {
+        } else if (HB > 1 || p.arrivals == nullptr) {
             const float to_true = fast_exp2(mr - mt);
             const int64_t prow = ((int64_t)c.token * p.nsplit + c.sp) * p.H + head;
             float* orow = p.part_o + prow * 512 + 256 * v + 4 * g;
@@ -2109,9 +2133,24 @@ __global__ __launch_bounds__(64 * XsLds<HB>::WAVES, 1) void sparse_mla_fwd_xs(Fw
                 p.part_m[prow] = mt * kLn2;
                 p.part_l[prow] = l * to_true;
             }
+        } else {
+            // In-kernel merge: the same partials, stored agent-coherent for the
+            // group's last workgroup (merge_group_cols reads them back).
+            const float to_true = fast_exp2(mr - mt);
+            const __amdgpu_buffer_rsrc_t rs = group_block(p, c.token, c.sp, head0, 16);
+            const uint32_t voff = (uint32_t)(n16 * 2048 + 16 * g + 64 * 16 * v);
+#pragma unroll
+            for (int cb = 0; cb < 16; ++cb)
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, oacc[hb][cb] * to_true), rs,
+                                                       voff + 64 * cb, 0, kAgentCoherent);
+            if (writes_ml) {
+                const int64_t prow = ((int64_t)c.token * p.nsplit + c.sp) * p.H + head;
+                __hip_atomic_store(p.part_m + prow, mt * kLn2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(p.part_l + prow, l * to_true, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
         }
     }
-    finish();
+    if (finish()) merge_group_cols<16, 2>(p, c, head0, 16, n16, g, v == 0 && g == 0, 16 * v);
 }
 
 // ============================================================== ping-pong
@@ -2161,6 +2200,10 @@ struct PPLds {
 // half-steps in which group 0 runs PV, off the critical QK path.
 __device__ __forceinline__ void pp_issue(const FwdParams& p, const Gather& gt, int t, uint32_t stage,
                                          uint32_t idx_lds, int gw, int lane) {
+    // Lane-dependent addresses from an opaque copy of the lane id: hoisted out
+    // of the pass loop they would be spilled, and each reload's vmcnt(0) would
+    // wait for the gathers just issued.
+    asm volatile("" : "+v"(lane));
     const int rows = p.kv_rows;
     const int r0 = 8 * gw;
     const int my_id = lds_load<int>(idx_lds + 4 * (t * PPLds::BN + r0 + (lane & 7)));

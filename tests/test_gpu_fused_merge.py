@@ -64,7 +64,11 @@ PLANS = [Tuning(16, 64, 2, kv_waves=4, mfma=16), Tuning(16, 64, 3, kv_waves=4, m
          Tuning(16, 64, 5, kv_waves=4, mfma=16), Tuning(16, 64, 16, kv_waves=4, mfma=16),
          Tuning(32, 64, 2, kv_waves=2, mfma=16), Tuning(32, 64, 8, kv_waves=2, mfma=16),
          Tuning(64, 64, 4, kv_waves=1, mfma=16), Tuning(64, 64, 7, kv_waves=1, mfma=16),
-         Tuning(16, 64, 2, kv_waves=4, mfma=16, pv_cols=128), Tuning(16, 64, 5, kv_waves=4, mfma=16, pv_cols=128)]
+         Tuning(16, 64, 2, kv_waves=4, mfma=16, pv_cols=128), Tuning(16, 64, 5, kv_waves=4, mfma=16, pv_cols=128),
+         # specialised waves (16 heads, 32-row tiles): the PV waves merge in the last workgroup
+         Tuning(16, 32, 2, kv_waves=2, stages=4, mfma=16, pv_cols=128),
+         Tuning(16, 32, 7, kv_waves=2, stages=4, mfma=16, pv_cols=128),
+         Tuning(16, 32, 16, kv_waves=2, stages=4, mfma=16, pv_cols=128)]
 
 
 @pytest.mark.parametrize("config", PLANS, ids=str)

@@ -92,7 +92,7 @@ def test_planner_covers_any_shape(shape):
     assert shape[2] % plan.bm == 0
     if plan.pv_cols == 128 and plan.bn == 32 and plan.bm < 128:  # specialised waves: 16 or 32 heads
         assert plan.kv_waves == 2 and plan.stages == 4 and plan.mfma == 16 and plan.bm in (16, 32)
-        assert not plan.fused_merge  # the merge kernel only
+        assert not plan.fused_merge or plan.bm == 16  # in-kernel merge: 16 heads only
     elif plan.pv_cols == 128 and plan.bm < 128:  # column-split PV: four waves share every head block
         assert plan.kv_waves == 4 and plan.mfma == 16 and plan.bm in (16, 32, 64)
     elif plan.pv_cols == 128:  # ping-pong
@@ -134,6 +134,12 @@ def test_plan_call_fused_merge_is_one_launch():
     # a fused plan goes through the same library check as any other
     with pytest.raises(ValueError, match="fused_merge"):
         plan_call(CASE_SHAPES["c2_decode_b8"], Tuning(64, 64, 2, kv_waves=2, mfma=32, fused_merge=True))
+    with pytest.raises(ValueError, match="fused_merge"):  # specialised waves: 16 heads only
+        plan_call(CASE_SHAPES["c2_decode_b8"],
+                  Tuning(32, 32, 8, kv_waves=2, stages=4, mfma=16, pv_cols=128, fused_merge=True))
+    config, _, launches = plan_call(CASE_SHAPES["c3_decode_h16_mtp"],
+                                    Tuning(16, 32, 2, kv_waves=2, stages=4, mfma=16, pv_cols=128, fused_merge=True))
+    assert len(launches) == 1 and launches[0].name.startswith("sparse_mla_fwd_xs_h16")
     with pytest.raises(ValueError, match="bool"):
         plan_call(shape, Tuning(16, 64, 2, kv_waves=4, mfma=16, fused_merge=1))
 
