@@ -107,6 +107,10 @@ CASES = [
     (((2, 40, 128, 8192, 2048), (1, 7, 128, 2048, 512)), Tuning(128, 32, 1, stages=4)),              # no split
     (((2, 16, 128, 8192, 2048), (1, 5, 128, 4096, 700)),
      Tuning(128, 32, 2, kv_waves=1, stages=4, mfma=16, pv_cols=128)),                                # ping-pong, split 2
+    (((8, 1, 128, 32768, 2048), (3, 1, 128, 4096, 1024)),
+     Tuning(32, 32, 8, kv_waves=2, stages=4, mfma=16, pv_cols=128)),                                 # specialised waves (C2's)
+    (((16, 2, 16, 8192, 2048), (5, 2, 16, 4096, 2000)),
+     Tuning(16, 32, 2, kv_waves=2, stages=4, mfma=16, pv_cols=128, fused_merge=True)),               # ... merged in the kernel
 ]
 
 
