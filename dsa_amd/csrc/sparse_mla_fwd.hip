@@ -1837,8 +1837,8 @@ __device__ __forceinline__ void xs_load(const FwdParams& p, const char* kv, cons
     const int r = r0 + (lane >> 3);
     const int id = lds_load<int>(idx_lds + 4 * (tt * 32 + r));
     const uint32_t voff = ((uint32_t)min(max(id, 0), rows - 1) << 7) + (((lane & 7) ^ sw_rope(r)) << 4);
-    const __amdgpu_buffer_rsrc_t rr = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(kr), (short)0,
-                                                                        live ? rows * 128 : 0, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<char*>(kr), (short)0, live ? (int)((uint32_t)rows * 128u) : 0, 0x00020000);  // < 2^32 bytes
     b.v[8] = __builtin_amdgcn_raw_buffer_load_b128(rr, voff, 0, 0);
     __builtin_amdgcn_sched_barrier(0);  // keep the issue order: the loads of later tiles stay in flight
 }

@@ -65,7 +65,9 @@ def _check(tag, got, ref):
     return check(tag, *got, ref)
 
 
-@pytest.mark.parametrize("H,config", [(16, None), (128, Tuning(128, 32, 1, stages=4))], ids=["h16-planner", "h128-wide"])
+@pytest.mark.parametrize("H,config", [(16, None), (128, Tuning(128, 32, 1, stages=4)),
+                                      (32, Tuning(32, 32, 2, kv_waves=2, stages=4, mfma=16, pv_cols=128))],
+                         ids=["h16-planner", "h128-wide", "h32-specialised"])
 def test_max_length_contiguous(H, config):
     B, SQ, K, L = 2, 2, 1024, L_MAX
     g = torch.Generator().manual_seed(H)
