@@ -1777,9 +1777,8 @@ __device__ __forceinline__ uint32_t pp_pchunk(int h, int g) {
 // kernel, or for 16 heads (arrival counters given) in the workgroup of each
 // (token, head group) that stores its partials last, as the column-split
 // kernel does (merge_if_last).
-// One QK or PV wave alone keeps a tile's LDS reads in flight, so its fragment
-// pipelines are deep (LDS latency under the gather writes is a few hundred
-// cycles; 14 reads of a wave may be outstanding).
+// Fragment pipelines: 12 K reads (QK) and 6 V fragment pairs (PV) in flight
+// per wave; 8 / 5 and 14 / 7 measured the same.
 #ifndef XS_QK_DEPTH
 #define XS_QK_DEPTH 12
 #endif
@@ -1823,7 +1822,7 @@ __device__ __forceinline__ void xs_load(const FwdParams& p, const char* kv, cons
     const int tt = max(min(t, nt - 1), 0);
     const int rows = p.kv_rows;
     const int r0 = 8 * j;
-    const int my_id = lds_load<int>(idx_lds + 4 * (tt * 32 + r0 + (lane & 7)));
+    const int my_id = lds_load<int>(idx_lds + 4 * (tt * XsLds<1>::BN + r0 + (lane & 7)));
     const uint32_t my_row = (uint32_t)min(max(my_id, 0), rows - 1);
     const uint32_t lane16 = (uint32_t)lane << 4;
     const int row_bytes = live ? 1024 : 0;
@@ -1835,7 +1834,7 @@ __device__ __forceinline__ void xs_load(const FwdParams& p, const char* kv, cons
         b.v[rr] = __builtin_amdgcn_raw_buffer_load_b128(rs, lane16 ^ ((uint32_t)sw_kv(r0 + rr) << 4), 0, 0);
     }
     const int r = r0 + (lane >> 3);
-    const int id = lds_load<int>(idx_lds + 4 * (tt * 32 + r));
+    const int id = lds_load<int>(idx_lds + 4 * (tt * XsLds<1>::BN + r));
     const uint32_t voff = ((uint32_t)min(max(id, 0), rows - 1) << 7) + (((lane & 7) ^ sw_rope(r)) << 4);
     const __amdgpu_buffer_rsrc_t rr = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<char*>(kr), (short)0, live ? (int)((uint32_t)rows * 128u) : 0, 0x00020000);  // < 2^32 bytes
@@ -1848,7 +1847,7 @@ __device__ __forceinline__ void xs_store(uint32_t stage, int j, int lane, const 
     const uint32_t st = stage + ((uint32_t)lane << 4);
 #pragma unroll
     for (int rr = 0; rr < 8; ++rr) lds_store<u32x4>(st + (8 * j + rr) * 1024, b.v[rr]);
-    lds_store<u32x4>(st + 32 * 1024 + 8 * j * 128, b.v[8]);
+    lds_store<u32x4>(st + XsLds<1>::KV_BYTES + 8 * j * 128, b.v[8]);  // ring layout: the same for every HB
     __builtin_amdgcn_sched_barrier(0);
 }
 
