@@ -30,6 +30,10 @@ leaves it out).  ``roofline.frac`` is the main kernel's (its average launch);
 The warm-up and every timed batch walk one continuous rotation over the input
 sets, so the warm-up leaves none of the first timed sets in the caches.
 
+``--cases all`` times the reference's 16 validated cases instead, one line
+each (span, main, merge with the selected plan) beside the reference's
+published Ascend950PR span for the case: context, not a baseline line.
+
 cpu_baseline: the CPU oracle (oracle/dsa_oracle.py, a restatement of the
 reference's FP32 PyTorch gather+softmax path) timed on this host on a bounded
 sample of the same workload, with every CPU the process may use (capped by
@@ -56,7 +60,7 @@ sys.path.insert(0, str(ROOT))
 import dsa_amd  # noqa: E402
 from dsa_amd import Tuning, _lib  # noqa: E402
 from dsa_amd.workloads import (BASELINE_CONFIGS, INDEXER_CONFIGS, baseline_inputs,  # noqa: E402
-                               indexer_inputs)
+                               case_inputs, indexer_inputs)
 
 METRIC = json.loads((ROOT / "BASELINE.json").read_text())["metric"]
 HBM_PEAK_GBS = 8000.0
@@ -64,6 +68,17 @@ MFMA_PEAK_TFLOPS = 2500.0  # dense bf16
 # Published device span of the reference on Ascend950PR for the same shape
 # (PERFORMANCE_FINAL.md:75 of the reference, decode_b8 task span).
 PUBLISHED_SPAN_US = {"c2_decode_b8": 74.875}
+# The reference's 16 validated cases (dsa/config.py:23-40) and its published
+# device span per call on Ascend950PR (PERFORMANCE_FINAL.md:74-89 of the
+# reference, refactored TLA column, merge included), for ``--cases``.
+REF_CASES = ("decode_b1", "decode_b8", "decode_b32", "decode_tp8", "prefill_q16", "prefill_q64", "prefill_tp8",
+             "prefill_k512", "decode_b4_h128", "decode_b4_h64", "decode_b4_h32", "decode_b4_h16",
+             "prefill_b4_h128", "prefill_b4_h64", "prefill_b4_h32", "prefill_b4_h16")
+REF_CASE_SPAN_US = {"decode_b1": 26.0, "decode_b8": 74.875, "decode_b32": 227.625, "decode_tp8": 47.25,
+                    "prefill_q16": 116.0, "prefill_q64": 362.25, "prefill_tp8": 403.25, "prefill_k512": 134.25,
+                    "decode_b4_h128": 51.25, "decode_b4_h64": 41.0, "decode_b4_h32": 35.25, "decode_b4_h16": 31.625,
+                    "prefill_b4_h128": 139711.0, "prefill_b4_h64": 111399.0, "prefill_b4_h32": 96924.6,
+                    "prefill_b4_h16": 89610.8}
 # Which roofline binds each configuration.
 BOUND = {"c1_decode_b1": "hbm", "c2_decode_b8": "hbm", "c3_decode_h16_mtp": "hbm",
          "c4_prefill_h16": "mfma", "c5_prefill_h128": "mfma"}
@@ -432,6 +447,34 @@ def run(name, args, overrides=True):
     return line
 
 
+def run_case(name, args):
+    """One of the reference's 16 cases at full size with the selected plan:
+    span, main and merge per call (timed as the workloads are), beside the
+    reference's published Ascend950PR span for the same case.  Input sets
+    (the review recipe's distribution, drawn on the device) are cycled until
+    their gathered rows exceed twice the 256 MB MALL, at most 32; the number
+    of timed calls is cut so that each timing takes about two seconds."""
+    shape = dsa_amd.CASE_SHAPES[name]
+    b, sq, h, length, k = shape
+    config = dsa_amd.select(shape)
+    rows_bytes = b * sq * k * 1152
+    rotate = max(1, min(32, -(-(512 << 20) // rows_bytes)))
+    if rotate * (b * length * 1152 + b * sq * h * 1152) > (32 << 30):  # big cases: one set
+        rotate = 1
+    sets = [case_inputs(shape, seed=args.seed + i) for i in range(rotate)]
+    calls = [Call(d, config) for d in sets]
+    once = time_calls(calls, 1, 1)[3]
+    steps = max(3, min(args.steps, int(2e6 / max(once, 1.0))))
+    warmup = max(1, min(args.warmup, steps))
+    _, main_us, merge_us, span_us = time_calls(calls, steps, warmup)
+    ref = REF_CASE_SPAN_US[name]
+    return {"case": name, "B": b, "SQ": sq, "H": h, "L": length, "TOPK": k, "plan": vars(config),
+            "span_us": round(span_us, 3), "main_us": round(main_us, 3), "merge_us": round(merge_us, 3),
+            "steps": steps, "warmup": warmup, "rotating_input_sets": rotate,
+            "reference_ascend950pr_span_us": ref, "span_vs_reference": round(span_us / ref, 4),
+            "data": "synthetic: seeded N(0,1) bf16 q/kv/rope, distinct uniform indices per token"}
+
+
 def uv_line(shape, config, dv, uv_us):
     """The W_UV launch of a call (the merge_us slot of the breakdown):
     algorithmic HBM bytes = the weights once, the latent input (bf16 output,
@@ -609,6 +652,8 @@ def main():
                     help="time the lightning indexer instead: " + ", ".join(INDEXER_CONFIGS) + " or all")
     ap.add_argument("--uv", type=int, default=0, metavar="DV",
                     help="append the W_UV output projection (value head dim DV, e.g. 128) to every call")
+    ap.add_argument("--cases", default="", metavar="NAMES",
+                    help="time the reference's 16 cases instead (comma list or all): one line each")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-prefill", action="store_true",
                     help="decode line only (by default it carries a prefill leg: C5 and C4)")
@@ -638,6 +683,13 @@ def main():
             if name not in INDEXER_CONFIGS:
                 raise SystemExit(f"unknown indexer workload {name!r}")
             print(json.dumps(run_indexer(name, args), ensure_ascii=False), flush=True)
+        return
+    if args.cases:
+        for name in list(REF_CASES) if args.cases == "all" else args.cases.split(","):
+            if name not in REF_CASE_SPAN_US:
+                raise SystemExit(f"unknown reference case {name!r}")
+            print(json.dumps(run_case(name, args), ensure_ascii=False), flush=True)
+            torch.cuda.empty_cache()
         return
     threads, counts = cpu_threads()
     torch.set_num_threads(threads)

@@ -70,6 +70,25 @@ def _subset_rows(n_rows, length, k, gen, device, limit=None):
     return keys.topk(k, dim=1, largest=False).indices.int()
 
 
+def case_inputs(shape, seed: int = REVIEW_SEED, device="cuda"):
+    """Inputs of any (B, SQ, H, L, TOPK) shape drawn on ``device`` from the
+    review recipe's distribution (family normal: N(0,1) bf16 q/kv/rope, per
+    token TOPK distinct indices uniform over [0, L)).  ``review_inputs`` draws
+    the same distribution on the CPU call for call as the reference does; this
+    one is for timing the reference's cases at full size (its largest, 4 x 8192
+    tokens x 128 heads, takes seconds here)."""
+    batch, queries, heads, length, k = shape
+    gen = torch.Generator(device=device).manual_seed(seed)
+    q = _normal_bf16((batch, queries, heads, 512), gen, device)
+    kv = _normal_bf16((batch, length, 1, 512), gen, device)
+    qr = _normal_bf16((batch, queries, heads, 64), gen, device)
+    kr = _normal_bf16((batch, length, 1, 64), gen, device)
+    tokens = batch * queries
+    rows = max(1, (64 << 20) // (4 * length))  # 64 MiB of sort keys per chunk
+    ids = torch.cat([_subset_rows(min(rows, tokens - i), length, k, gen, device) for i in range(0, tokens, rows)])
+    return q, kv, qr, kr, ids.reshape(batch, queries, 1, k).contiguous()
+
+
 def baseline_inputs(name: str, seed: int = REVIEW_SEED, device="cuda", cpu_recipe: bool = True):
     """Inputs of MI355X benchmark configuration ``name`` on ``device``.
 

@@ -80,6 +80,26 @@ def test_baseline_configs_in_table(name):
     assert dsa_amd.select(CASE_SHAPES[name]) == SELECTED[name]
 
 
+def test_case_inputs_distribution():
+    """The device-side draw of the review recipe (bench.py --cases): shapes,
+    dtypes, TOPK distinct indices per token inside [0, L), reproducible per
+    seed."""
+    from dsa_amd.workloads import case_inputs
+    shape = (2, 3, 16, 300, 40)
+    q, kv, qr, kr, ids = case_inputs(shape, seed=7, device="cpu")
+    assert q.shape == (2, 3, 16, 512) and kv.shape == (2, 300, 1, 512)
+    assert qr.shape == (2, 3, 16, 64) and kr.shape == (2, 300, 1, 64)
+    assert ids.shape == (2, 3, 1, 40) and ids.dtype == torch.int32
+    assert {t.dtype for t in (q, kv, qr, kr)} == {torch.bfloat16}
+    rows = ids.reshape(6, 40)
+    assert int(rows.min()) >= 0 and int(rows.max()) < 300
+    assert all(len(set(r.tolist())) == 40 for r in rows)
+    assert len({tuple(r.tolist()) for r in rows}) == 6
+    assert abs(float(q.float().std()) - 1.0) < 0.05
+    again = case_inputs(shape, seed=7, device="cpu")
+    assert all(torch.equal(a, b) for a, b in zip((q, kv, qr, kr, ids), again))
+
+
 @pytest.mark.parametrize("shape", [(1, 1, 16, 1, 1), (3, 5, 48, 1000, 777), (2, 7, 32, 9, 4097),
                                    (1, 1, 128, 65536, 8192), (64, 2, 16, 65536, 2048)])
 def test_planner_covers_any_shape(shape):
