@@ -80,6 +80,19 @@ def test_baseline_configs_in_table(name):
     assert dsa_amd.select(CASE_SHAPES[name]) == SELECTED[name]
 
 
+def test_bench_reference_cases_cover_the_table():
+    """bench.py --cases times exactly the reference's 16 validated cases, each
+    with a published span to compare against."""
+    import importlib.util
+    from pathlib import Path
+    spec = importlib.util.spec_from_file_location("bench", Path(__file__).resolve().parents[1] / "bench.py")
+    bench = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(bench)
+    ref = {n for n in CASE_SHAPES if n[:2] not in ("c1", "c2", "c3", "c4", "c5")}
+    assert set(bench.REF_CASES) == ref == set(bench.REF_CASE_SPAN_US)
+    assert len(bench.REF_CASES) == 16 and all(v > 0 for v in bench.REF_CASE_SPAN_US.values())
+
+
 def test_case_inputs_distribution():
     """The device-side draw of the review recipe (bench.py --cases): shapes,
     dtypes, TOPK distinct indices per token inside [0, L), reproducible per
