@@ -16,16 +16,27 @@ the span per call (the ``value``).  The main kernel alone and the merge alone
 are timed the same way (K launches each), which gives the main kernel's
 average duration for the roofline.  An event between every launch would add
 its own few microseconds to each interval, so none is recorded inside a
-batch.  ``ms_per_step`` is the host wall clock of the K timed calls.
+batch.  ``ms_per_step`` is the host wall clock of the K timed calls (median
+over the rounds).
 ``breakdown.kernel_sum_us`` adds the two kernels' launch-alone durations, and
 ``breakdown.eager_call_us`` is the median wall clock of one ``dsa_amd.forward``
 call (checks, allocation, launches) followed by a device synchronisation.
 
+Every quantity is timed in R rounds (``--rounds``, default 5) of K calls,
+interleaved (span, main alone, merge alone, then the next round); the line
+gives the median and, in ``breakdown``, the min and max over the rounds.
+
 The metric is "decode B=8 + prefill": the default line is C2 (``value``)
-and carries a ``prefill`` object with the C5 and C4 lines' span, roofline
-(MFMA-bound), breakdown and CPU baseline, timed the same way (``--no-prefill``
-leaves it out).  ``roofline.frac`` is the main kernel's (its average launch);
-``roofline.frac_span`` is the whole call's, split merge included.
+and carries the other GPU configurations timed the same way, as flat scalar
+fields: ``decode`` holds C3 (``c3_span_us``, ``c3_span_min_us``,
+``c3_frac``, ``c3_cpu_us`` ...) and C2's spread and fixed chain,
+``prefill`` holds C5 and C4 (``c5_...``, ``c4_...``); ``roofline`` repeats
+their ``frac`` / ``frac_span`` and ``cpu_baseline`` their CPU values
+(``--no-legs`` leaves them out).  ``roofline.frac`` is the main kernel's
+(its average launch); ``roofline.frac_span`` is the whole call's, split
+merge included.  ``breakdown.fixed_chain_us`` is C2's plan on the same input
+sets with one tile per workgroup (TOPK = split x tile rows): the part of a
+call that does not scale with the gathered rows.
 
 The warm-up and every timed batch walk one continuous rotation over the input
 sets, so the warm-up leaves none of the first timed sets in the caches.
@@ -35,10 +46,11 @@ each (span, main, merge with the selected plan) beside the reference's
 published Ascend950PR span for the case: context, not a baseline line.
 
 cpu_baseline: the CPU oracle (oracle/dsa_oracle.py, a restatement of the
-reference's FP32 PyTorch gather+softmax path) timed on this host on a bounded
-sample of the same workload, with every CPU the process may use (capped by
-OMP_NUM_THREADS when the host sets it); the line records the counts and the
-CPU model.
+reference's FP32 PyTorch gather+softmax path) timed on this host on full
+calls of the same workload (one warm-up call, then the median of 5 calls, or
+of 3 for the 4096-query prefills), with every CPU the process may use
+(capped by OMP_NUM_THREADS when the host sets it); the line records the
+counts and the CPU model.
 """
 from __future__ import annotations
 
@@ -214,15 +226,17 @@ def _batch_us(rot, steps, stream_obj, work):
     return e0.elapsed_time(e1) * 1e3 / steps
 
 
-def time_calls(calls, steps, warmup):
-    """W untimed warm-up calls, then exactly K timed calls (main kernel +
-    merge) back to back between two HIP events, with device synchronisation
-    on both sides: returns (host wall seconds of those K calls, span µs per
-    call).  Then K main-kernel launches alone and K merges alone, timed the
-    same way: (main µs, merge µs) per launch, the main kernel's average
-    duration being the roofline's denominator.  All of it walks one
-    continuous rotation over the input sets (``Rotation``): the warm-up does
-    not leave the first timed sets in the cache."""
+def time_rounds(calls, steps, warmup, rounds=1):
+    """W untimed warm-up calls, then R rounds, each of exactly K calls
+    (main kernel + merge) back to back between two HIP events with device
+    synchronisation on both sides, followed by K main-kernel launches alone
+    and K merges alone timed the same way (the rounds interleave the three,
+    as the reference's review interleaves its samples).  Returns per-call
+    device µs lists ``span``, ``main``, ``merge`` (one entry per round) and
+    ``wall``, the host seconds of each round's K calls.  The main kernel's
+    launches give its average duration, the roofline's denominator.  All of
+    it walks one continuous rotation over the input sets (``Rotation``): the
+    warm-up does not leave the first timed sets in the cache."""
     stream_obj = torch.cuda.current_stream()
     stream = ctypes.c_void_p(stream_obj.cuda_stream)
     rot = Rotation(calls)
@@ -230,12 +244,26 @@ def time_calls(calls, steps, warmup):
     for _ in range(warmup):
         both(rot.take(), stream)
     torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    span = _batch_us(rot, steps, stream_obj, both)
-    wall = time.perf_counter() - t0
-    main = _batch_us(rot, steps, stream_obj, lambda c, s: c.main(s))
-    merge = _batch_us(rot, steps, stream_obj, lambda c, s: c.merge(s))
-    return wall, main, merge, span
+    out = {"span": [], "main": [], "merge": [], "wall": []}
+    for _ in range(rounds):
+        t0 = time.perf_counter()
+        out["span"].append(_batch_us(rot, steps, stream_obj, both))
+        out["wall"].append(time.perf_counter() - t0)
+        out["main"].append(_batch_us(rot, steps, stream_obj, lambda c, s: c.main(s)))
+        out["merge"].append(_batch_us(rot, steps, stream_obj, lambda c, s: c.merge(s)))
+    return out
+
+
+def time_calls(calls, steps, warmup):
+    """One round of ``time_rounds``: (host wall seconds of the K calls, main
+    µs, merge µs, span µs) per call."""
+    t = time_rounds(calls, steps, warmup, 1)
+    return t["wall"][0], t["main"][0], t["merge"][0], t["span"][0]
+
+
+def spread(values):
+    """Median, min and max of one quantity over the rounds."""
+    return statistics.median(values), min(values), max(values)
 
 
 def cpu_model():
@@ -290,8 +318,10 @@ def eager_us(data, config, samples=30):
     return statistics.median(times) * 1e6
 
 
-def cpu_baseline(name, data, budget_s=10.0):
-    """Time the CPU oracle on a bounded sample; scale to µs per full call."""
+def cpu_baseline(name, data, samples=None):
+    """The CPU oracle on full calls of the workload: one warm-up call, then
+    the median of 5 calls (C1-C3) or 3 calls (C4, C5), as the reference's
+    baseline protocol asks; the inputs are on the host beforehand."""
     from oracle import dsa_oracle as oracle
 
     fp8 = data[3] is None  # kv holds fp8 rows: the oracle runs on their dequantized values
@@ -300,31 +330,21 @@ def cpu_baseline(name, data, budget_s=10.0):
         q, qr, ids = (t.cpu() for t in (data[0], data[2], data[4]))
     else:
         q, kv, qr, kr, ids = (t.cpu() for t in data)
-    batch, queries = q.shape[:2]
-    tokens = [(b, s) for b in range(batch) for s in range(queries)]
-    # sample: whole call when small, else an evenly spaced token subset
-    probe_t = time.perf_counter()
-    oracle.reference(q, kv, qr, kr, ids, tokens=tokens[:1])
-    per_token = max(time.perf_counter() - probe_t, 1e-4)
-    n = len(tokens)
-    if per_token * n > budget_s / 3:
-        n = max(1, int(budget_s / 3 / per_token))
-    sample = tokens[:: max(1, len(tokens) // n)][:n]
+    if samples is None:
+        samples = 3 if q.shape[1] >= 1024 else 5
+    oracle.reference(q, kv, qr, kr, ids)  # warm-up
     times = []
-    t_end = time.perf_counter() + budget_s
-    oracle.reference(q, kv, qr, kr, ids, tokens=sample)  # warm-up
-    while time.perf_counter() < t_end or len(times) < 3:
+    for _ in range(samples):
         t0 = time.perf_counter()
-        oracle.reference(q, kv, qr, kr, ids, tokens=sample)
+        oracle.reference(q, kv, qr, kr, ids)
         times.append(time.perf_counter() - t0)
-        if len(times) >= 50:
-            break
-    per_call_us = statistics.median(times) * 1e6 * len(tokens) / len(sample)
+    per_call_us = statistics.median(times) * 1e6
     return {"value": round(per_call_us, 1), "unit": "µs/call", "cores": torch.get_num_threads(),
             "kind": "port", "cpu": cpu_model(), **CPU_COUNTS,
-            "sample": (f"FP32 torch gather+softmax oracle on {len(sample)} of {len(tokens)} tokens of one "
-                       f"{name} call, median of {len(times)} runs after one warm-up, scaled to a full call; "
-                       f"inputs already on the host (generation and copies not timed)"
+            "min_us": round(min(times) * 1e6, 1), "max_us": round(max(times) * 1e6, 1),
+            "sample": (f"full call: FP32 torch gather+softmax oracle over all {q.shape[0] * q.shape[1]} tokens of "
+                       f"one {name} call, one warm-up call then the median of {samples}; inputs already on the "
+                       f"host (generation and copies not timed)"
                        + ("; kv dequantized from the fp8 rows beforehand (not timed)" if fp8 else ""))}
 
 
@@ -356,9 +376,32 @@ def paged(data, block_size, seed):
     return (q, kv_pool, qr, kr_pool, ids), perm.view(batch, per).int().contiguous()
 
 
+def plan_text(config):
+    """A plan as one string (a JSON record keeps it where nested objects are
+    dropped)."""
+    return (f"bm={config.bm} bn={config.bn} split={config.split} kv_waves={config.kv_waves} "
+            f"stages={config.stages} mfma={config.mfma} pv_cols={config.pv_cols} "
+            f"fused_merge={int(config.fused_merge)}")
+
+
+def fixed_chain_us(calls, config, args):
+    """The same plan on the same input sets with only TOPK = split x tile_rows
+    slots per token (one tile per workgroup): the per-call cost that does not
+    scale with the gathered rows (launches, the cold index and first-tile
+    round trips, the partial stores and the merge).  Median span over the
+    rounds."""
+    slots = config.split * config.bn
+    short = []
+    for c in calls:
+        q, kv, qr, kr, ids = c.data
+        short.append(Call((q, kv, qr, kr, ids[..., :slots].contiguous()), config))
+    t = time_rounds(short, args.steps, args.warmup, args.rounds)
+    return statistics.median(t["span"]), slots
+
+
 def run(name, args, overrides=True):
     """One workload's line.  ``overrides=False`` ignores --plan and --rotate
-    (the prefill leg that follows a decode line uses its own defaults)."""
+    (the legs that follow the headline line use their own defaults)."""
     shape = BASELINE_CONFIGS[name]
     rotate = args.rotate if args.rotate and overrides else DEFAULT_ROTATE[name]
     config = dsa_amd.select(shape, kv_fp8=args.fp8)
@@ -385,8 +428,13 @@ def run(name, args, overrides=True):
                 sets[i] = None
     else:
         calls = [Call(d, config, fp8=args.fp8, uv_dim=args.uv) for d in sets]
-    wall, main_us, merge_us, span_us = time_calls(calls, args.steps, args.warmup)
-    _, warm_main, _, warm_span = time_calls(calls[:1], args.steps, args.warmup)
+    t = time_rounds(calls, args.steps, args.warmup, args.rounds)
+    span_us, span_min, span_max = spread(t["span"])
+    main_us, main_min, main_max = spread(t["main"])
+    merge_us = statistics.median(t["merge"])
+    wall = statistics.median(t["wall"])
+    warm = time_rounds(calls[:1], args.steps, args.warmup, args.rounds)
+    warm_span, warm_main = statistics.median(warm["span"]), statistics.median(warm["main"])
     gbytes, flops = algorithmic_units(shape, args.fp8)
     bound = BOUND[name]
     if bound == "hbm":
@@ -414,7 +462,7 @@ def run(name, args, overrides=True):
                  + ("; kv cache as 656-byte fp8 rows (e4m3 latent, fp32 block scales, bf16 rope)"
                     if args.fp8 else "")),
         "config": {"workload": name, "B": shape[0], "SQ": shape[1], "H": shape[2], "L": shape[3],
-                   "TOPK": shape[4], "plan": vars(config) if hasattr(config, "__dict__") else str(config),
+                   "TOPK": shape[4], "plan": plan_text(config), "rounds": args.rounds,
                    "rotating_input_sets": rotate, "paged_block_size": args.paged or None,
                    "kv_format": "fp8" if args.fp8 else "bf16"},
         "roofline": {"bound": bound, "achieved": round(achieved, 2), "peak": peak, "unit": unit,
@@ -422,13 +470,17 @@ def run(name, args, overrides=True):
                      "achieved_span": round(achieved_span, 2), "frac_span": round(achieved_span / peak, 4),
                      "kernel": (f"sparse_mla_fwd (main), {gbytes} gathered B and {flops} FLOP per launch; "
                                 f"frac on the main kernel's average launch, frac_span on the whole call "
-                                f"(split merge included)"),
+                                f"(split merge included); medians of {args.rounds} rounds"),
                      "traffic_source": (f"profiles/sparse_mla_fwd_{name}_hbm_traffic.json (build of commit "
                                         f"{traffic_commit})" if traffic is not None else None)},
         **({"dtype_note": "kv stored as fp8 e4m3 rows; MFMA inputs bf16"} if args.fp8 else {}),
         "breakdown": {
             "span_us": round(span_us, 3),
+            "span_min_us": round(span_min, 3),
+            "span_max_us": round(span_max, 3),
             "main_us": round(main_us, 3),
+            "main_min_us": round(main_min, 3),
+            "main_max_us": round(main_max, 3),
             "merge_us": round(merge_us, 3),
             "kernel_sum_us": round(main_us + merge_us, 3),
             "warm_span_us": round(warm_span, 3),
@@ -440,11 +492,29 @@ def run(name, args, overrides=True):
             "mfma_TFLOPs_span": round(flops / (span_us * 1e-6) / 1e12, 2),
         },
     }
+    if bound == "hbm" and config.split > 1 and not (args.paged or args.fp8 or args.uv):
+        chain, slots = fixed_chain_us(calls, config, args)
+        line["breakdown"]["fixed_chain_us"] = round(chain, 3)
+        line["breakdown"]["fixed_chain_topk"] = slots
     if args.uv:
         line["w_uv"] = uv_line(shape, config, args.uv, merge_us)
     if not args.no_cpu_baseline:
-        line["cpu_baseline"] = cpu_baseline(name, sets[0], args.cpu_budget)
+        line["cpu_baseline"] = cpu_baseline(name, sets[0])
     return line
+
+
+def leg(prefix, line):
+    """A workload's line as flat scalar fields named ``<prefix>_...``, for the
+    headline line's ``decode`` and ``prefill`` objects."""
+    r, b, c = line["roofline"], line["breakdown"], line.get("cpu_baseline") or {}
+    out = {"span_us": line["value"], "span_min_us": b["span_min_us"], "span_max_us": b["span_max_us"],
+           "main_us": b["main_us"], "merge_us": b["merge_us"], "bound": r["bound"], "achieved": r["achieved"],
+           "unit": r["unit"], "frac": r["frac"], "frac_span": r["frac_span"], "traffic": r["traffic"],
+           "plan": line["config"]["plan"], "rotating_input_sets": line["config"]["rotating_input_sets"],
+           "cpu_us": c.get("value"), "cpu_sample": c.get("sample")}
+    if "fixed_chain_us" in b:
+        out["fixed_chain_us"] = b["fixed_chain_us"]
+    return {f"{prefix}_{k}": v for k, v in out.items()}
 
 
 def run_case(name, args):
@@ -655,9 +725,10 @@ def main():
     ap.add_argument("--cases", default="", metavar="NAMES",
                     help="time the reference's 16 cases instead (comma list or all): one line each")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--no-prefill", action="store_true",
-                    help="decode line only (by default it carries a prefill leg: C5 and C4)")
-    ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU oracle timing")
+    ap.add_argument("--rounds", type=int, default=5, help="timed rounds of K calls (median, min, max reported)")
+    ap.add_argument("--no-legs", action="store_true",
+                    help="C2 line only (by default it carries C3, C5 and C4 legs)")
+    ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of indexer CPU oracle timing")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run 5 device copies of MIB MiB (reference kernel for rocprofv3 byte counters)")
     args = ap.parse_args()
@@ -697,22 +768,26 @@ def main():
     names = ["c2_decode_b8", "c3_decode_h16_mtp", "c4_prefill_h16", "c5_prefill_h128"] if args.all else [args.config]
     for name in names:
         line = run(name, args)
-        if not args.all and not args.no_prefill and BOUND[name] == "hbm":
-            # The metric is "decode B=8 + prefill": the decode line carries the
-            # prefill configurations as a leg of their own (C5 first: the
-            # MFMA-bound headline; C4: 16 heads, L2/MALL-bound).
-            line["prefill"] = {p: prefill_leg(run(p, args, overrides=False))
-                               for p in ("c5_prefill_h128", "c4_prefill_h16")}
+        if not args.all and not args.no_legs and name == "c2_decode_b8":
+            # The metric is "decode B=8 + prefill": the headline line carries
+            # the other GPU configurations as flat legs timed the same way:
+            # C3 (16-head MTP decode, HBM-bound) in ``decode``, C5 (the
+            # MFMA-bound prefill) and C4 (16 heads, L2/MALL-bound) in
+            # ``prefill``; their roofline fractions also go into ``roofline``.
+            legs = {p: run(p, args, overrides=False)
+                    for p in ("c3_decode_h16_mtp", "c5_prefill_h128", "c4_prefill_h16")}
+            line["decode"] = {**leg("c3", legs["c3_decode_h16_mtp"]),
+                              "c2_span_min_us": line["breakdown"]["span_min_us"],
+                              "c2_span_max_us": line["breakdown"]["span_max_us"],
+                              "c2_fixed_chain_us": line["breakdown"].get("fixed_chain_us")}
+            line["prefill"] = {**leg("c5", legs["c5_prefill_h128"]), **leg("c4", legs["c4_prefill_h16"])}
+            for p, l in (("c3", legs["c3_decode_h16_mtp"]), ("c5", legs["c5_prefill_h128"]),
+                         ("c4", legs["c4_prefill_h16"])):
+                line["roofline"][f"{p}_frac"] = l["roofline"]["frac"]
+                line["roofline"][f"{p}_frac_span"] = l["roofline"]["frac_span"]
+                if "cpu_baseline" in line and "cpu_baseline" in l:
+                    line["cpu_baseline"][f"{p}_value"] = l["cpu_baseline"]["value"]
         print(json.dumps(line, ensure_ascii=False), flush=True)
-
-
-PREFILL_KEYS = ("value", "unit", "steps", "warmup", "ms_per_step", "config", "roofline", "breakdown", "cpu_baseline")
-
-
-def prefill_leg(line):
-    """The parts of a prefill workload's line that go into the decode line's
-    ``prefill`` object (the rest repeats the decode line's own keys)."""
-    return {k: line[k] for k in PREFILL_KEYS if k in line}
 
 
 if __name__ == "__main__":

@@ -27,6 +27,13 @@ _LDS_BYTES = 2 * 64 * 1152 + 2048 * 4
 _PP_LDS_BYTES = 4 * 32 * 1152 + 2048 * 4 + 2 * 64 * 64  # ring, index cache, two P buffers
 
 
+def _xp_lds_bytes(bm):
+    # ring (two 64-row stages), index cache (halved for 64 heads), P of one
+    # tile (144 bytes a head), per-wave maxima, vote flag (XpLds<bm / 16>)
+    idx_cap = 2048 if bm <= 32 else 1024
+    return 2 * 64 * 1152 + idx_cap * 4 + bm * 144 + 4 * bm * 4 + 16
+
+
 def _xs_lds_bytes(bm):
     # ring, index cache, two P buffers, (l, reference max, max) per head, vote flag
     return 4 * 32 * 1152 + 2048 * 4 + 2 * bm * 64 + 3 * bm * 4 + 16
@@ -59,22 +66,22 @@ def _check_inputs(q, kv, q_rope, k_rope, indices, block_table=None):
         raise ValueError("with fp8 kv rows (uint8 [..., 656]) k_rope must be None: the rope values are in the rows")
     if not fp8 and k_rope is None:
         raise ValueError("k_rope is required unless kv holds fp8 rows (uint8 [..., 656])")
-    q_shape, kv_shape, ids_shape = tuple(q.shape), tuple(kv.shape), tuple(indices.shape)
+    q_shape, kv_shape, ids_shape = q.shape, kv.shape, indices.shape
     if len(q_shape) != 4 or len(kv_shape) != 4 or len(ids_shape) != 4:
         raise ValueError("q, kv and indices must be 4-D tensors")
     batch, queries, heads, width = q_shape
-    topk = ids_shape[-1]
+    topk = ids_shape[3]
     if block_table is None:
         length = kv_shape[1]
         pool = (batch, length)
     else:
         if block_table.dim() != 2 or block_table.shape[0] != batch:
             raise ValueError("block_table must be [B, max_blocks]")
-        pool = kv_shape[:2]
+        pool = (kv_shape[0], kv_shape[1])
         length = block_table.shape[1] * kv_shape[1]
     if (width != HEAD_DIM or kv_shape != (*pool, 1, FP8_ROW if fp8 else HEAD_DIM)
-            or tuple(q_rope.shape) != (batch, queries, heads, ROPE_DIM)
-            or (not fp8 and tuple(k_rope.shape) != (*pool, 1, ROPE_DIM))
+            or q_rope.shape != (batch, queries, heads, ROPE_DIM)
+            or (not fp8 and k_rope.shape != (*pool, 1, ROPE_DIM))
             or ids_shape != (batch, queries, 1, topk)
             or min(batch, queries, heads, length, topk, *pool) <= 0):
         if fp8:
@@ -88,10 +95,13 @@ def _check_inputs(q, kv, q_rope, k_rope, indices, block_table=None):
     if heads % 16:
         raise ValueError(f"the number of heads must be a multiple of 16 (got {heads})")
     device = q.device
-    tensors = (kv, q_rope) + (() if fp8 else (k_rope,)) + (indices,) + (() if block_table is None else (block_table,))
     if (device.type != "cuda" or torch.version.hip is None
-            or any(t.device != device for t in tensors)
-            or not all(t.is_contiguous() for t in (q,) + tensors)):
+            or kv.device != device or q_rope.device != device or indices.device != device
+            or (not fp8 and k_rope.device != device)
+            or (block_table is not None and block_table.device != device)
+            or not (q.is_contiguous() and kv.is_contiguous() and q_rope.is_contiguous()
+                    and indices.is_contiguous() and (fp8 or k_rope.is_contiguous())
+                    and (block_table is None or block_table.is_contiguous()))):
         raise ValueError("all inputs must be contiguous and on the same ROCm GPU")
     bf16 = torch.bfloat16
     if (q.dtype != bf16 or (not fp8 and kv.dtype != bf16) or q_rope.dtype != bf16
@@ -151,8 +161,8 @@ def plan_call(shape, config=None, cores: int = 256, kv_fp8: bool = False, w_uv_d
         config = select(shape, cores, kv_fp8)
     else:
         check_tuning(config, shape)
-        if kv_fp8 and config.mfma != 16:
-            raise ValueError("fp8 kv rows need a narrow plan (mfma=16)")
+        if kv_fp8 and (config.mfma != 16 or config.pv_cols != 512):
+            raise ValueError("fp8 kv rows need a narrow plan (mfma 16, pv_cols 512)")
     batch, queries, heads, _, _ = shape
     tokens = batch * queries
     if config.pv_cols == 128:
@@ -160,8 +170,10 @@ def plan_call(shape, config=None, cores: int = 256, kv_fp8: bool = False, w_uv_d
     else:
         variant = "wide" if config.mfma == 32 else "narrow"
     threads, lds = (512, _PP_LDS_BYTES) if variant == "pp" else (256, _LDS_BYTES)
-    if variant == "xp" and config.bm == 16:
-        threads = 512  # four compute waves and four gather waves
+    if variant == "xp":
+        lds = _xp_lds_bytes(config.bm)
+        if config.bm == 16:
+            threads = 512  # four compute waves and four gather waves
     if variant == "xs":  # QK waves (one per 16 heads), two PV waves, four gather waves
         threads, lds = 64 * (config.bm // 16 + 6), _xs_lds_bytes(config.bm)
     launches = [Launch(f"sparse_mla_fwd_{variant}_h{config.bm}_kw{config.kv_waves}_bn{config.bn}_s{config.stages}",
@@ -288,7 +300,8 @@ def forward(q, kv, q_rope, k_rope, indices, *, config=None, cores=None, return_k
     ``config``: a :class:`dsa_amd.Tuning` (default: the shape's table entry or
     the library planner).  ``cores``: CU budget for planning (default: the
     device's CU count).  ``return_kernels=True`` also returns the launch
-    descriptors.  Outputs are fresh tensors; nothing is cached across calls and
+    descriptors.  Outputs are fresh tensors; no input or result is kept across
+    calls (only the plan of each shape, and the arrival counters below), and
     the call does not synchronise.
 
     Beyond the reference: ``scale`` (positive float) replaces the fixed 1/24,
@@ -325,10 +338,9 @@ def forward(q, kv, q_rope, k_rope, indices, *, config=None, cores=None, return_k
     uv = None if w_uv is None else _check_w_uv(w_uv, heads, device)
     _check_arrivals(arrivals, device)
     if cores is None:
-        cores = torch.cuda.get_device_properties(device).multi_processor_count
-    config, partials, launches = plan_call(shape, config, cores, fp8, None if uv is None else uv[0])
-    fused = config.fused_merge and config.split > 1 and uv is None
-    groups = batch * queries * (heads // config.bm)
+        cores = _device_cus(device)
+    config, partials, launches, plan, fused, groups = _call_plan(shape, config, cores, fp8,
+                                                                 None if uv is None else uv[0])
     if fused and arrivals is not None and arrivals.numel() < groups:
         raise ValueError(f"arrivals holds {arrivals.numel()} counters; this call needs {groups}")
 
@@ -338,57 +350,43 @@ def forward(q, kv, q_rope, k_rope, indices, *, config=None, cores=None, return_k
     if partials is None:
         part_o = part_m = part_l = None
     else:
-        part_o = torch.empty(partials[0], device=device, dtype=torch.float32)
-        part_m = torch.empty(partials[1], device=device, dtype=torch.float32)
-        part_l = torch.empty_like(part_m)
+        # One buffer carved into part_o, part_m, part_l (each 256-byte aligned):
+        # only their addresses leave this function.
+        part_buf = torch.empty(partials[2], device=device, dtype=torch.float32)
+        part_o = part_buf.data_ptr()
+        part_m = part_o + partials[3]
+        part_l = part_o + partials[4]
 
-    def ptr(t):
-        return None if t is None else ctypes.c_void_p(t.data_ptr())
-
-    plan = config.to_c()
-    stream = torch.cuda.current_stream(device).cuda_stream
-    args = (ptr(q), ptr(kv), ptr(q_rope), ptr(k_rope), ptr(indices),
-            ptr(output), ptr(maximum), ptr(denominator), ptr(part_o), ptr(part_m), ptr(part_l),
-            batch, queries, heads, length, topk)
+    stream = torch._C._cuda_getCurrentRawStream(device.index)
+    args = (q.data_ptr(), kv.data_ptr(), q_rope.data_ptr(), None if k_rope is None else k_rope.data_ptr(),
+            indices.data_ptr(), output.data_ptr(), maximum.data_ptr(), denominator.data_ptr(),
+            part_o, part_m, part_l, batch, queries, heads, length, topk)
     merge_uv = uv is not None and config.split > 1
-    with torch.cuda.device(device):
+    lib = _lib.load()
+    with _on_device(device):
         if merge_uv:
             # Main kernel only; the merge runs inside the W_UV launch below.
-            opts = _lib.DsaFwdOptions()
-            opts.scale = 0.0 if scale is None else scale
-            opts.kv_format = _lib.KV_FP8 if fp8 else _lib.KV_BF16
-            if block_table is not None:
-                opts.block_size = kv.shape[1]
-                opts.max_blocks = block_table.shape[1]
-                opts.num_blocks = kv.shape[0]
-                opts.block_table = block_table.data_ptr()
-            rc = _lib.load().dsa_fwd_main_opts(*args, ctypes.byref(opts), ctypes.byref(plan),
-                                               ctypes.c_void_p(stream))
+            opts = _options(scale, fp8, kv, block_table)
+            rc = lib.dsa_fwd_main_opts(*args, ctypes.byref(opts), plan, stream)
         elif scale is None and block_table is None and not fp8 and not fused:
-            rc = _lib.load().dsa_fwd(*args, ctypes.byref(plan), ctypes.c_void_p(stream))
+            rc = lib.dsa_fwd(*args, plan, stream)
         else:
-            opts = _lib.DsaFwdOptions()
-            opts.scale = 0.0 if scale is None else scale
-            opts.kv_format = _lib.KV_FP8 if fp8 else _lib.KV_BF16
-            if block_table is not None:
-                opts.block_size = kv.shape[1]
-                opts.max_blocks = block_table.shape[1]
-                opts.num_blocks = kv.shape[0]
-                opts.block_table = block_table.data_ptr()
+            opts = _options(scale, fp8, kv, block_table)
             if fused:
                 counters = arrivals if arrivals is not None else _arrival_counters(device, stream, groups)
                 opts.arrivals = counters.data_ptr()
-            rc = _lib.load().dsa_fwd_opts(*args, ctypes.byref(opts), ctypes.byref(plan), ctypes.c_void_p(stream))
-    _lib.check(rc, "dsa_fwd_main" if merge_uv else "dsa_fwd")
+            rc = lib.dsa_fwd_opts(*args, ctypes.byref(opts), plan, stream)
+    if rc:
+        _lib.check(rc, "dsa_fwd_main" if merge_uv else "dsa_fwd")
     if uv is None:
         result = (output, maximum, denominator)
     elif merge_uv:
         dv, head_stride = uv
         out_v = torch.empty((batch, queries, heads, dv), device=device, dtype=torch.bfloat16)
-        with torch.cuda.device(device):
-            rc = _lib.load().dsa_merge_uv(ptr(part_o), ptr(part_m), ptr(part_l), _vp(w_uv), head_stride,
-                                          _vp(out_v), ptr(maximum), ptr(denominator), batch * queries, heads,
-                                          config.split, dv, ctypes.c_void_p(stream))
+        with _on_device(device):
+            rc = lib.dsa_merge_uv(part_o, part_m, part_l, w_uv.data_ptr(), head_stride, out_v.data_ptr(),
+                                  maximum.data_ptr(), denominator.data_ptr(), batch * queries, heads,
+                                  config.split, dv, stream)
         _lib.check(rc, "dsa_merge_uv")
         result = (out_v, maximum, denominator)
     else:
@@ -396,6 +394,93 @@ def forward(q, kv, q_rope, k_rope, indices, *, config=None, cores=None, return_k
     if return_kernels:
         return result, launches
     return result
+
+
+def _options(scale, fp8, kv, block_table):
+    opts = _lib.DsaFwdOptions()
+    opts.scale = 0.0 if scale is None else scale
+    opts.kv_format = _lib.KV_FP8 if fp8 else _lib.KV_BF16
+    if block_table is not None:
+        opts.block_size = kv.shape[1]
+        opts.max_blocks = block_table.shape[1]
+        opts.num_blocks = kv.shape[0]
+        opts.block_table = block_table.data_ptr()
+    return opts
+
+
+# Plans of the calls seen so far, keyed by everything plan_call reads: a
+# repeated shape skips the table lookup, the plan checks and the descriptor
+# construction (the reference checks its table once, at import:
+# dsa/api.py:63-73).  Entries are immutable; a bounded dict, cleared when full.
+_PLAN_CACHE_MAX = 4096
+_plan_cache = {}
+
+
+def _call_plan(shape, config, cores, fp8, uv_dim):
+    """plan_call's result for one call, with the C plan struct (passed by
+    reference, read only), whether the merge runs in the main kernel and the
+    number of (token, head group) pairs.  ``partials`` becomes (part_o shape,
+    part_m shape, floats of the one buffer holding all three, byte offsets of
+    part_m and part_l in it) when the plan splits."""
+    if type(cores) is not int or cores <= 0:
+        raise ValueError("cores must be a positive int")
+    if config is not None and not isinstance(config, Tuning):
+        raise TypeError("config must be a dsa_amd.Tuning")
+    # A Tuning equals one whose int fields are given as bools or floats (True
+    # == 1), which check_tuning rejects: the field types are part of the key.
+    key = (shape, config, None if config is None else tuple(map(type, vars(config).values())), cores, fp8,
+           uv_dim)
+    hit = _plan_cache.get(key)
+    if hit is not None:
+        return hit
+    config, partials, launches = plan_call(shape, config, cores, fp8, uv_dim)
+    if partials is not None:
+        o_elems = 1
+        for d in partials[0]:
+            o_elems *= d
+        m_elems = o_elems // HEAD_DIM
+        align = 64  # floats: 256 bytes
+        o_pad = -(-o_elems // align) * align
+        m_pad = -(-m_elems // align) * align
+        partials = (partials[0], partials[1], o_pad + 2 * m_pad, 4 * o_pad, 4 * (o_pad + m_pad))
+    batch, queries, heads, _, _ = shape
+    fused = config.fused_merge and config.split > 1 and uv_dim is None
+    hit = (config, partials, launches, config.to_c(), fused,
+           batch * queries * (heads // config.bm))
+    if len(_plan_cache) >= _PLAN_CACHE_MAX:
+        _plan_cache.clear()
+    _plan_cache[key] = hit
+    return hit
+
+
+_device_cu_counts = {}
+
+
+def _device_cus(device) -> int:
+    n = _device_cu_counts.get(device.index)
+    if n is None:
+        n = torch.cuda.get_device_properties(device).multi_processor_count
+        _device_cu_counts[device.index] = n
+    return n
+
+
+class _NoDeviceSwitch:
+    def __enter__(self):
+        return None
+
+    def __exit__(self, *exc):
+        return False
+
+
+_SAME_DEVICE = _NoDeviceSwitch()
+
+
+def _on_device(device):
+    """``torch.cuda.device(device)`` unless it is already the current device
+    (the library launches on the current HIP device)."""
+    if torch.cuda.current_device() == device.index:
+        return _SAME_DEVICE
+    return torch.cuda.device(device)
 
 
 def _check_partials(part_o, part_m, part_l):

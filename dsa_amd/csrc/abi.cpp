@@ -52,7 +52,7 @@ int check_shape(int B, int SQ, int H, int L, int TOPK) {
 
 extern "C" {
 
-int dsa_version(void) { return (1 << 16) | 0; }
+int dsa_version(void) { return (1 << 16) | 1; }
 
 const char* dsa_last_error(void) { return g_err; }
 

@@ -13,6 +13,16 @@
  * over the TOPK slots I_j = indices[t, j].  Duplicate slots keep their weight.
  * Every row needs at least one valid slot (an all-invalid row returns NaN).
  *
+ * Magnitude bound.  The kernels form exp(score - m_ref) against a reference
+ * max m_ref taken from the first tile and recompute a range once with the
+ * exact max only when a score exceeds m_ref by more than 64 log2 units, so a
+ * weight before the division by sum can reach 2^64 (the reference's never
+ * exceeds 1).  A workgroup covers S <= DSA_IDX_CAP = 2048 slots, and its FP32
+ * output accumulators stay finite whenever
+ *   max|kv| * S < 2^128 / 2^64,  i.e. for every call  max|kv| < 2^53 (9.0e15),
+ * against max|kv| * TOPK < 2^128 (3.4e38) for the FP32 reference.  Beyond the
+ * bound the output may be inf or NaN; max and sum are unaffected.
+ *
  * Conventions of every entry point:
  *   - plain pointers to device memory; bf16 tensors are passed as uint16_t
  *     bit patterns; all tensors dense row-major (contiguous);
@@ -87,7 +97,8 @@ typedef struct dsa_plan {
     int32_t pv_cols;
 } dsa_plan;
 
-/* Library version, (major << 16) | minor. */
+/* Library version, (major << 16) | minor.  1.1: dsa_plan.pv_cols (a reserved
+ * zero field in 1.0, which still selects the same plans) and dsa_fwd_noalloc. */
 int dsa_version(void);
 
 /* Thread-local text of the last failure on this thread ("" if none). */
@@ -229,8 +240,7 @@ int dsa_fwd_main_opts(const uint16_t* q, const uint16_t* kv, const uint16_t* q_r
 /*
  * dsa_fwd_opts for callers that cannot allocate: code under HIP graph
  * capture, tight serving loops, harnesses that forbid hipMalloc.  No
- * counterpart in the reference (its forward allocates the partials with
- * torch.empty on every call, dsa/api.py:101-113).
+ * counterpart in the reference.
  *
  * Same arguments and results as dsa_fwd_opts without part_o / part_m /
  * part_l: the split partials -- and the arrival counters of a plan with

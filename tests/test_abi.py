@@ -36,8 +36,36 @@ def test_library_exports_every_declared_symbol():
 
 def test_version_and_last_error():
     lib = _lib.load()
-    assert lib.dsa_version() >> 16 == 1
+    # 1.1: dsa_plan.pv_cols and dsa_fwd_noalloc
+    assert lib.dsa_version() == (1 << 16) | 1
     assert isinstance(lib.dsa_last_error(), bytes)
+
+
+def test_magnitude_bound_follows_the_restart_clamp():
+    """The header's kv magnitude bound is the one the kernels' restart clamp
+    implies: a weight before the division by the sum reaches at most
+    2^kRestartLog2, a workgroup sums at most DSA_IDX_CAP of them into an FP32
+    accumulator, so max|kv| < 2^(128 - kRestartLog2 - log2(DSA_IDX_CAP)).
+    An FP32 emulation of one accumulator shows both sides of the bound."""
+    import math
+
+    import numpy as np
+
+    src = (HEADER.parents[1] / "dsa_amd" / "csrc" / "sparse_mla_fwd.hip").read_text()
+    clamp = float(re.search(r"constexpr float kRestartLog2 = ([0-9.]+)f;", src).group(1))
+    header = HEADER.read_text()
+    cap = int(re.search(r"#define DSA_IDX_CAP (\d+)", header).group(1))
+    bound_log2 = 128 - clamp - math.log2(cap)
+    assert bound_log2 == 53
+    assert "max|kv| < 2^53 (9.0e15)" in header and f"more than {int(clamp)} log2 units" in header
+    weight = np.float32(2.0 ** clamp)
+    with np.errstate(over="ignore"):
+        for log2_kv, finite in ((bound_log2 - 0.01, True), (bound_log2 + 0.01, False)):
+            acc = np.float32(0.0)
+            term = np.float32(weight * np.float32(2.0 ** log2_kv))
+            for _ in range(cap):  # one workgroup's slots, each at the largest weight
+                acc = np.float32(acc + term)
+            assert bool(np.isfinite(acc)) == finite, (log2_kv, acc)
 
 
 def test_struct_layout_matches_header():

@@ -108,3 +108,7 @@ def test_fp8_rejects_wide_plans():
     rows = dsa_amd.quantize_kv_fp8(kv.cuda(), kr.cuda())
     with pytest.raises(ValueError, match="narrow"):
         dsa_amd.forward(q.cuda(), rows, qr.cuda(), None, ids.cuda(), config=Tuning(128, 32, 1, stages=4))
+    # column-split PV (pv_cols 128) reads bf16 rows only
+    with pytest.raises(ValueError, match="narrow"):
+        dsa_amd.forward(q.cuda(), rows, qr.cuda(), None, ids.cuda(),
+                        config=Tuning(16, 64, 2, kv_waves=4, mfma=16, pv_cols=128))

@@ -147,6 +147,13 @@ def test_plan_call_allocations_and_launches():
     # 16 heads, column-split PV: four compute waves and four gather waves
     _, _, launches = plan_call(shape, config=Tuning(16, 64, 4, kv_waves=4, mfma=16, pv_cols=128), cores=256)
     assert launches[0].name.startswith("sparse_mla_fwd_xp_h16") and launches[0].block == 512
+    # XpLds<HB>: two 64-row stages, the index cache (1024 slots for 64 heads),
+    # P at 144 bytes a head, four waves' maxima, the vote flag
+    for bm, idx_cap in ((16, 2048), (32, 2048), (64, 1024)):
+        _, _, launches = plan_call(shape, config=Tuning(bm, 64, 4, kv_waves=4, mfma=16, pv_cols=128), cores=256)
+        assert launches[0].lds_bytes == 2 * 64 * 1152 + idx_cap * 4 + bm * 144 + 4 * bm * 4 + 16
+        assert launches[0].lds_bytes <= 160 * 1024
+    assert launches[0].lds_bytes == 161808
     # 16 heads, specialised waves: one QK wave, two PV and four gather waves
     _, _, launches = plan_call(shape, config=Tuning(16, 32, 4, kv_waves=2, stages=4, mfma=16, pv_cols=128), cores=256)
     assert launches[0].name.startswith("sparse_mla_fwd_xs_h16") and launches[0].block == 448

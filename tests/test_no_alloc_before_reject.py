@@ -159,6 +159,11 @@ def test_gpu_rejections_allocate_and_launch_nothing(spy):
                                            "arrivals": torch.zeros(5, dtype=torch.int32, device="cuda")}, ValueError))
     cases.append(("arrivals-device", base, {"config": fused, "arrivals": torch.zeros(6, dtype=torch.int32)},
                   ValueError))
+    # fp8 kv rows with a plan whose kernels read bf16 rows only
+    rows = torch.zeros(2, 300, 1, 656, dtype=torch.uint8, device="cuda")
+    fp8_args = [base[0], rows, base[2], None, base[4]]
+    cases.append(("config-fp8-pv_cols", fp8_args, {"config": Tuning(16, 64, 2, kv_waves=4, mfma=16, pv_cols=128)},
+                  ValueError))
     for name, args, kwargs, exc in cases:
         _expect_rejected(spy, name, args, kwargs, exc)
     print(f"[no allocation before rejection] {len(cases)} mutations rejected with nothing allocated or launched",
