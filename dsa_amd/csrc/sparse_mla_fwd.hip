@@ -312,13 +312,13 @@ __device__ __forceinline__ IdxRegs<CAP> fetch_indices(const FwdParams& p, const 
 // conditional store would let the compiler sink each global load into its
 // branch and wait for it there, serialising the loads.
 template <int BN, int CAP>
-__device__ __forceinline__ void store_indices(const IdxRegs<CAP>& r, uint32_t idx_lds, const FwdParams& p,
-                                              const WgCoords& c) {
+__device__ __forceinline__ IdxRegs<CAP> mask_indices(const IdxRegs<CAP>& r, const FwdParams& p, const WgCoords& c) {
     // Cached value: the kv row to gather (the pool row when paged), or -1 for
     // a masked slot (index < 0 or >= L, slot past TOPK or past the range).
     constexpr int N = CAP / kThreads;
     const int nslots = c.nt * BN;
-    int out[N];
+    IdxRegs<CAP> res;
+    int* out = res.v;
     if (p.block_table == nullptr) {
 #pragma unroll
         for (int i = 0; i < N; ++i) {
@@ -351,9 +351,70 @@ __device__ __forceinline__ void store_indices(const IdxRegs<CAP>& r, uint32_t id
             out[i] = ok ? row : -1;
         }
     }
+    return res;
+}
+template <int BN, int CAP>
+__device__ __forceinline__ void store_indices(const IdxRegs<CAP>& r, uint32_t idx_lds, const FwdParams& p,
+                                              const WgCoords& c) {
+    const IdxRegs<CAP> m = mask_indices<BN>(r, p, c);
 #pragma unroll
-    for (int i = 0; i < N; ++i)
-        lds_store<int>(idx_lds + 4 * ((int)threadIdx.x + i * kThreads), out[i]);
+    for (int i = 0; i < CAP / kThreads; ++i)
+        lds_store<int>(idx_lds + 4 * ((int)threadIdx.x + i * kThreads), m.v[i]);
+}
+
+// Compaction of the workgroup's slots (threads 0..255 hold the masked cache
+// values of mask_indices): the valid entries, in slot order, go to the front
+// of the cache and the last tile is padded with -1, so masked slots cost no
+// gather and no MFMA work.  A masked slot contributes exactly nothing (its
+// score is -inf), so the result changes only by the order of the FP32 sums.
+// Two halves around a workgroup barrier that every wave passes:
+// compact_count (threads 0..255: each wave publishes the valid count of each
+// of its N chunks to `counts`, 4 N ints of LDS) and, after the barrier,
+// compact_store (threads 0..255: entries to their ranks, padding) and
+// compact_total (every thread: the valid count, for the tile count).
+template <int CAP>
+__device__ __forceinline__ void compact_count(const IdxRegs<CAP>& m, uint32_t counts) {
+    constexpr int N = CAP / kThreads;
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        const uint64_t b = __ballot(m.v[i] >= 0);
+        if (lane == i) lds_store<int>(counts + 4 * (w * N + i), __popcll(b));
+    }
+}
+template <int CAP>
+__device__ __forceinline__ int compact_total(uint32_t counts) {
+    constexpr int N = CAP / kThreads;
+    int total = 0;
+#pragma unroll
+    for (int k = 0; k < 4 * N; k += 4) {
+        const i32x4 v = lds_load<i32x4>(counts + 4 * k);
+        total += v[0] + v[1] + v[2] + v[3];
+    }
+    return total;
+}
+template <int BN, int CAP>
+__device__ __forceinline__ void compact_store(const IdxRegs<CAP>& m, uint32_t counts, uint32_t idx_lds, int total) {
+    constexpr int N = CAP / kThreads;
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    int base = 0;  // valid entries of the earlier chunks
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        int before = 0, all = 0;  // this chunk: in earlier waves, in every wave
+#pragma unroll
+        for (int ww = 0; ww < 4; ++ww) {
+            const int n = lds_load<int>(counts + 4 * (ww * N + i));
+            before += ww < w ? n : 0;
+            all += n;
+        }
+        const uint64_t b = __ballot(m.v[i] >= 0);
+        const int rank = base + before +
+                         (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(b >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)b, 0u));
+        if (m.v[i] >= 0) lds_store<int>(idx_lds + 4 * rank, m.v[i]);
+        base += all;
+    }
+    const int pad = total + (int)threadIdx.x;
+    if ((int)threadIdx.x < BN && pad < (total + BN - 1) / BN * BN) lds_store<int>(idx_lds + 4 * pad, -1);
 }
 
 // Buffer resources over this workgroup's batch of kv and k_rope.
@@ -2276,7 +2337,19 @@ __global__ __launch_bounds__(kPPThreads, 1) void sparse_mla_fwd_pp(FwdParams p) 
         qf[16] = *reinterpret_cast<const bf16x8*>(rrow);
         qf[17] = *reinterpret_cast<const bf16x8*>(rrow + 32);
     }
-    if (wave < 4) store_indices<BN>(ids, idx_lds, p, c);
+    // Masked slots compacted away (compact_count): the workgroup runs
+    // nt = ceil(valid / 32) tiles.  The counts live in group 1's P buffer,
+    // which is first written after the barrier that ends the prologue.
+    const uint32_t counts = lds + X::P_OFF + X::P_GROUP;
+    IdxRegs<> masked;
+    if (wave < 4) {
+        masked = mask_indices<BN>(ids, p, c);
+        compact_count(masked, counts);
+    }
+    lds_barrier();
+    const int valid = compact_total<DSA_IDX_CAP>(counts);
+    if (wave < 4) compact_store<BN>(masked, counts, idx_lds, valid);
+    const int nt = __builtin_amdgcn_readfirstlane((valid + BN - 1) / BN);
     lds_barrier();
     const Gather gt = make_gather(p, c.b);
 
@@ -2406,7 +2479,7 @@ __global__ __launch_bounds__(kPPThreads, 1) void sparse_mla_fwd_pp(FwdParams p) 
         if (grp == 0)
 #pragma unroll
             for (int i = 0; i < 3; ++i)
-                if (i < c.nt) pp_issue(p, gt, i, X::stage(lds, i), idx_lds, gw, lane);
+                if (i < nt) pp_issue(p, gt, i, X::stage(lds, i), idx_lds, gw, lane);
         // Q (and the first tiles) complete here; see the wide variant.
         wait_vmcnt<0>();
 
@@ -2415,30 +2488,30 @@ __global__ __launch_bounds__(kPPThreads, 1) void sparse_mla_fwd_pp(FwdParams p) 
         // group 0 issues tile t + 3 into the stage of tile t - 1, whose last
         // reader (group 1's PV) ran in half 2t.
         if (grp == 0) {
-            for (int t = 0; t < c.nt; ++t) {
-                const int ahead = min(2, c.nt - 1 - t);
+            for (int t = 0; t < nt; ++t) {
+                const int ahead = min(2, nt - 1 - t);
                 if (ahead >= 2) wait_vmcnt<2 * X::LOADS_PER_TILE>();
                 else if (ahead == 1) wait_vmcnt<X::LOADS_PER_TILE>();
                 else wait_vmcnt<0>();
                 lds_barrier();
                 qk_softmax(t, overflow);
                 lds_barrier();
-                if (t + 3 < c.nt) pp_issue(p, gt, t + 3, X::stage(lds, t + 3), idx_lds, gw, lane);
+                if (t + 3 < nt) pp_issue(p, gt, t + 3, X::stage(lds, t + 3), idx_lds, gw, lane);
                 pv(t);
             }
-            if (c.nt > 0) lds_barrier();  // half 2 nt: group 1's last PV
-        } else if (c.nt > 0) {
+            if (nt > 0) lds_barrier();  // half 2 nt: group 1's last PV
+        } else if (nt > 0) {
             lds_barrier();
             lds_barrier();
             qk_softmax(0, overflow);
-            for (int t = 1; t < c.nt; ++t) {
+            for (int t = 1; t < nt; ++t) {
                 lds_barrier();
                 pv(t - 1);
                 lds_barrier();
                 qk_softmax(t, overflow);
             }
             lds_barrier();
-            pv(c.nt - 1);
+            pv(nt - 1);
         }
         // ---- workgroup vote: does any head need pass 1?  (The flag lives in
         // the P buffers, free once every wave is past its last PV.)
