@@ -12,9 +12,11 @@ set) span is reported beside it.
 
 Timing: K calls are launched back to back on one stream between two HIP
 events (device-synchronised on both sides); the elapsed device time over K is
-the span per call (the ``value``).  The main kernel alone and the merge alone
-are timed the same way (K launches each), which gives the main kernel's
-average duration for the roofline.  An event between every launch would add
+the span per call (the ``value``).  A call is what ``dsa_amd.forward``
+enqueues: one ``dsa_fwd`` (main kernel + merge kernel, or the main kernel
+alone with an in-kernel merge).  The main kernel alone (``dsa_fwd_main``)
+and the merge alone are timed the same way (K launches each), which gives
+the main kernel's average duration for the roofline.  An event between every launch would add
 its own few microseconds to each interval, so none is recorded inside a
 batch.  ``ms_per_step`` is the host wall clock of the K timed calls (median
 over the rounds).
@@ -163,6 +165,24 @@ class Call:
             self.out_v = torch.empty((b, sq, h, uv_dim), device=dev, dtype=torch.bfloat16)
             self.uv_args = (p(self.w), uv_dim * 512, p(self.out_v))
 
+    def full(self, stream):
+        """One whole call as ``dsa_amd.forward`` enqueues it: dsa_fwd (or
+        dsa_fwd_opts) -- the main kernel and its merge in one C call -- or,
+        with the W_UV projection, the main kernel and the merge + W_UV
+        launch."""
+        if self.uv:
+            self.main(stream)
+            self.merge(stream)
+            return
+        b, sq, h, length, k = self.shape
+        if self.opts is None:
+            rc = self.lib.dsa_fwd(*self.args, b, sq, h, length, k, ctypes.byref(self.plan), stream)
+        else:
+            rc = self.lib.dsa_fwd_opts(*self.args, b, sq, h, length, k, ctypes.byref(self.opts),
+                                       ctypes.byref(self.plan), stream)
+        if rc:
+            _lib.check(rc, "dsa_fwd")
+
     def main(self, stream):
         b, sq, h, length, k = self.shape
         if self.fused:
@@ -240,7 +260,13 @@ def time_rounds(calls, steps, warmup, rounds=1):
     stream_obj = torch.cuda.current_stream()
     stream = ctypes.c_void_p(stream_obj.cuda_stream)
     rot = Rotation(calls)
-    both = lambda c, s: (c.main(s), c.merge(s))  # noqa: E731
+
+    def both(c, s):  # one whole call
+        if hasattr(c, "full"):
+            c.full(s)
+        else:
+            c.main(s)
+            c.merge(s)
     for _ in range(warmup):
         both(rot.take(), stream)
     torch.cuda.synchronize()
