@@ -518,7 +518,7 @@ def run(name, args, overrides=True):
             "mfma_TFLOPs_span": round(flops / (span_us * 1e-6) / 1e12, 2),
         },
     }
-    if bound == "hbm" and config.split > 1 and not (args.paged or args.fp8 or args.uv):
+    if bound == "hbm" and config.split > 1 and not (args.paged or args.fp8 or args.uv or args.no_chain):
         chain, slots = fixed_chain_us(calls, config, args)
         line["breakdown"]["fixed_chain_us"] = round(chain, 3)
         line["breakdown"]["fixed_chain_topk"] = slots
@@ -752,6 +752,8 @@ def main():
                     help="time the reference's 16 cases instead (comma list or all): one line each")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--rounds", type=int, default=5, help="timed rounds of K calls (median, min, max reported)")
+    ap.add_argument("--no-chain", action="store_true",
+                    help="leave out breakdown.fixed_chain_us (its launches are the same kernel: kernel traces)")
     ap.add_argument("--no-legs", action="store_true",
                     help="C2 line only (by default it carries C3, C5 and C4 legs)")
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of indexer CPU oracle timing")
