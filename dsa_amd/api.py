@@ -332,6 +332,15 @@ def forward(q, kv, q_rope, k_rope, indices, *, config=None, cores=None, return_k
     call gets counters of its own in the graph's pool.  Ignored by plans that
     do not fuse the merge.
     """
+    if (config is None and cores is None and not return_kernels and scale is None and block_table is None
+            and w_uv is None and arrivals is None):
+        fast = _fast_path()
+        if fast is not None:  # a planned shape: checks, outputs and launch in C++ (None: not taken)
+            r = fast.forward(q, kv, q_rope, k_rope, indices)
+            if r is not None:
+                if type(r) is int:
+                    _lib.check(r, "dsa_fwd")
+                return r
     scale = _check_scale(scale)
     shape, device, fp8 = _check_inputs(q, kv, q_rope, k_rope, indices, block_table)
     batch, queries, heads, length, topk = shape
@@ -339,10 +348,14 @@ def forward(q, kv, q_rope, k_rope, indices, *, config=None, cores=None, return_k
     _check_arrivals(arrivals, device)
     if cores is None:
         cores = _device_cus(device)
+    default_plan = config is None
     config, partials, launches, plan, fused, groups = _call_plan(shape, config, cores, fp8,
                                                                  None if uv is None else uv[0])
     if fused and arrivals is not None and arrivals.numel() < groups:
         raise ValueError(f"arrivals holds {arrivals.numel()} counters; this call needs {groups}")
+    if (default_plan and cores == _device_cus(device) and not fused and not fp8 and scale is None
+            and block_table is None and uv is None):
+        _register_fast(device, shape, plan, partials)
 
     output = torch.empty_like(q)
     maximum = torch.empty((batch, 1, queries, heads), device=device, dtype=torch.float32)
@@ -462,6 +475,46 @@ def _device_cus(device) -> int:
         n = torch.cuda.get_device_properties(device).multi_processor_count
         _device_cu_counts[device.index] = n
     return n
+
+
+# The host fast path (dsa_amd/_fast*.so, built from csrc/fast_forward.cpp):
+# forward() for a shape the Python path has already planned on that device
+# with the default plan and no options, checked, allocated and launched in
+# C++.  It returns None for anything the Python path would reject or has not
+# planned, so errors always come from the Python path.  Absent (not built),
+# every call takes the Python path.
+_fast_lock = threading.Lock()
+_fast_state = []  # [module or None] once loaded
+
+
+def _fast_path():
+    if _fast_state:
+        return _fast_state[0]
+    with _fast_lock:
+        if not _fast_state:
+            module = None
+            from . import build as _build
+
+            path = _build.fast_path_module()
+            if path.exists():
+                import importlib.util
+
+                spec = importlib.util.spec_from_file_location("dsa_amd._fast", path)
+                module = importlib.util.module_from_spec(spec)
+                spec.loader.exec_module(module)
+                module.set_entry(ctypes.cast(_lib.load().dsa_fwd, ctypes.c_void_p).value)
+            _fast_state.append(module)
+    return _fast_state[0]
+
+
+def _register_fast(device, shape, plan, partials):
+    fast = _fast_path()
+    if fast is None:
+        return
+    fields = [plan.heads_per_group, plan.tile_rows, plan.split, plan.kv_waves, plan.stages, plan.mfma,
+              plan.fused_merge, plan.pv_cols]
+    part = (0, 0, 0) if partials is None else partials[2:]
+    fast.register_plan(device.index, *shape, fields, *part)
 
 
 class _NoDeviceSwitch:

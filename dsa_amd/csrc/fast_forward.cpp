@@ -1,0 +1,136 @@
+// Host fast path of dsa_amd.forward for a repeated call (no reference
+// counterpart: the reference's forward is Python, dsa/api.py:76-132).
+//
+// forward() checks its inputs, allocates the outputs and calls dsa_fwd in
+// Python, which costs more host time than the decode kernels it launches.
+// This extension does the same work in C++ for the common call -- five
+// contiguous bf16 / int32 tensors on one ROCm GPU, default plan, no
+// options -- once the Python path has planned that shape on that device and
+// registered the plan here.  It never raises for a bad input: whatever the
+// Python path would reject (or has not planned yet) returns None and the
+// caller takes the Python path, which raises the reference's errors.  A
+// failed launch returns the library's status code, which the caller turns
+// into the library's error.  Nothing is allocated or launched before every
+// check has passed.
+#include <torch/extension.h>
+#include <c10/core/DeviceGuard.h>
+#include <c10/hip/HIPStream.h>
+
+#include <array>
+#include <cstdint>
+#include <mutex>
+#include <unordered_map>
+
+namespace {
+
+// int dsa_fwd(q, kv, q_rope, k_rope, idx, out, out_max, out_sum, part_o,
+//             part_m, part_l, B, SQ, H, L, TOPK, const dsa_plan*, void* stream)
+using FwdFn = int (*)(const void*, const void*, const void*, const void*, const void*, void*, void*, void*, void*,
+                      void*, void*, int, int, int, int, int, const void*, void*);
+FwdFn g_fwd = nullptr;
+
+struct Entry {
+    std::array<int32_t, 8> plan;  // the fields of struct dsa_plan, in order
+    int64_t part_floats;          // floats of the one partial buffer, 0 without a split
+    int64_t off_m, off_l;         // byte offsets of part_m and part_l in it
+};
+
+struct Key {
+    int64_t dev, B, SQ, H, L, K;
+    bool operator==(const Key& o) const {
+        return dev == o.dev && B == o.B && SQ == o.SQ && H == o.H && L == o.L && K == o.K;
+    }
+};
+struct KeyHash {
+    size_t operator()(const Key& k) const {
+        size_t h = 1469598103934665603ull;
+        for (int64_t v : {k.dev, k.B, k.SQ, k.H, k.L, k.K}) h = (h ^ (size_t)v) * 1099511628211ull;
+        return h;
+    }
+};
+
+constexpr size_t kMaxPlans = 4096;
+std::mutex g_mu;
+std::unordered_map<Key, Entry, KeyHash> g_plans;
+
+bool dims(const at::Tensor& t, std::initializer_list<int64_t> want) {
+    if (t.dim() != (int64_t)want.size()) return false;
+    int i = 0;
+    for (int64_t w : want)
+        if (t.size(i++) != w) return false;
+    return true;
+}
+
+py::object forward(const at::Tensor& q, const at::Tensor& kv, const at::Tensor& q_rope, const at::Tensor& k_rope,
+                   const at::Tensor& idx) {
+    if (g_fwd == nullptr || q.dim() != 4 || kv.dim() != 4 || idx.dim() != 4) return py::none();
+    const int64_t B = q.size(0), SQ = q.size(1), H = q.size(2), L = kv.size(1), K = idx.size(3);
+    if (q.size(3) != 512 || !dims(kv, {B, L, 1, 512}) || !dims(q_rope, {B, SQ, H, 64}) ||
+        !dims(k_rope, {B, L, 1, 64}) || !dims(idx, {B, SQ, 1, K}))
+        return py::none();
+    if (B <= 0 || SQ <= 0 || H <= 0 || L <= 0 || K <= 0 || H % 16 != 0) return py::none();
+    const c10::Device dev = q.device();
+    if (!dev.is_cuda() || kv.device() != dev || q_rope.device() != dev || k_rope.device() != dev ||
+        idx.device() != dev)
+        return py::none();
+    if (!q.is_contiguous() || !kv.is_contiguous() || !q_rope.is_contiguous() || !k_rope.is_contiguous() ||
+        !idx.is_contiguous())
+        return py::none();
+    if (q.scalar_type() != at::kBFloat16 || kv.scalar_type() != at::kBFloat16 ||
+        q_rope.scalar_type() != at::kBFloat16 || k_rope.scalar_type() != at::kBFloat16 ||
+        idx.scalar_type() != at::kInt)
+        return py::none();
+    Entry e;
+    {
+        std::lock_guard<std::mutex> lock(g_mu);
+        const auto it = g_plans.find(Key{dev.index(), B, SQ, H, L, K});
+        if (it == g_plans.end()) return py::none();
+        e = it->second;
+    }
+    c10::DeviceGuard guard(dev);
+    at::Tensor out = at::empty_like(q);
+    at::Tensor mx = at::empty({B, 1, SQ, H}, q.options().dtype(at::kFloat));
+    at::Tensor sm = at::empty_like(mx);
+    at::Tensor part;
+    char* pbase = nullptr;
+    if (e.part_floats > 0) {
+        part = at::empty({e.part_floats}, q.options().dtype(at::kFloat));
+        pbase = static_cast<char*>(part.data_ptr());
+    }
+    void* stream = c10::hip::getCurrentHIPStream(dev.index()).stream();
+    const int rc = g_fwd(q.data_ptr(), kv.data_ptr(), q_rope.data_ptr(), k_rope.data_ptr(), idx.data_ptr(),
+                         out.data_ptr(), mx.data_ptr(), sm.data_ptr(), pbase, pbase ? pbase + e.off_m : nullptr,
+                         pbase ? pbase + e.off_l : nullptr, (int)B, (int)SQ, (int)H, (int)L, (int)K, e.plan.data(),
+                         stream);
+    if (rc != 0) return py::int_(rc);
+    return py::make_tuple(out, mx, sm);
+}
+
+void set_entry(uint64_t dsa_fwd_address) { g_fwd = reinterpret_cast<FwdFn>(dsa_fwd_address); }
+
+void register_plan(int64_t dev, int64_t B, int64_t SQ, int64_t H, int64_t L, int64_t K, std::vector<int32_t> plan,
+                   int64_t part_floats, int64_t off_m, int64_t off_l) {
+    TORCH_CHECK(plan.size() == 8, "a dsa_plan has 8 fields");
+    Entry e;
+    std::copy(plan.begin(), plan.end(), e.plan.begin());
+    e.part_floats = part_floats;
+    e.off_m = off_m;
+    e.off_l = off_l;
+    std::lock_guard<std::mutex> lock(g_mu);
+    if (g_plans.size() >= kMaxPlans) g_plans.clear();
+    g_plans[Key{dev, B, SQ, H, L, K}] = e;
+}
+
+void clear_plans() {
+    std::lock_guard<std::mutex> lock(g_mu);
+    g_plans.clear();
+}
+
+}  // namespace
+
+PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
+    m.def("forward", &forward, "dsa_amd.forward for a planned shape, or None");
+    m.def("set_entry", &set_entry, "address of the library's dsa_fwd");
+    m.def("register_plan", &register_plan, "plan of a (device, B, SQ, H, L, TOPK) call");
+    m.def("clear_plans", &clear_plans, "forget every registered plan");
+}

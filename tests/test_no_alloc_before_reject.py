@@ -65,6 +65,9 @@ def spy(monkeypatch):
     real_load = _lib.load
     monkeypatch.setattr(A, "torch", TorchSpy(events))
     monkeypatch.setattr(A._lib, "load", lambda: LibSpy(real_load(), events))
+    # the C++ fast path allocates where the spy cannot see it: the Python
+    # path here (tests/test_gpu_fast_path.py covers the fast path's refusals)
+    monkeypatch.setattr(A, "_fast_path", lambda: None)
     return events
 
 
