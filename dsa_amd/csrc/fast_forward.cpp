@@ -61,8 +61,16 @@ bool dims(const at::Tensor& t, std::initializer_list<int64_t> want) {
     return true;
 }
 
-py::object forward(const at::Tensor& q, const at::Tensor& kv, const at::Tensor& q_rope, const at::Tensor& k_rope,
-                   const at::Tensor& idx) {
+// Arguments as plain handles: None (fp8 rows have no k_rope) or any other
+// non-tensor declines instead of raising pybind's TypeError.
+py::object forward(py::handle hq, py::handle hkv, py::handle hqr, py::handle hkr, py::handle hidx) {
+    for (py::handle h : {hq, hkv, hqr, hkr, hidx})
+        if (!THPVariable_Check(h.ptr())) return py::none();
+    const at::Tensor& q = THPVariable_Unpack(hq.ptr());
+    const at::Tensor& kv = THPVariable_Unpack(hkv.ptr());
+    const at::Tensor& q_rope = THPVariable_Unpack(hqr.ptr());
+    const at::Tensor& k_rope = THPVariable_Unpack(hkr.ptr());
+    const at::Tensor& idx = THPVariable_Unpack(hidx.ptr());
     if (g_fwd == nullptr || q.dim() != 4 || kv.dim() != 4 || idx.dim() != 4) return py::none();
     const int64_t B = q.size(0), SQ = q.size(1), H = q.size(2), L = kv.size(1), K = idx.size(3);
     if (q.size(3) != 512 || !dims(kv, {B, L, 1, 512}) || !dims(q_rope, {B, SQ, H, 64}) ||

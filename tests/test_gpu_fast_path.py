@@ -86,3 +86,26 @@ def test_fast_path_declines_every_rejected_input(fast):
         with pytest.raises((ValueError, TypeError)):
             dsa_amd.forward(*args)
     print(f"[fast path] {len(cases)} rejected inputs declined with nothing allocated", flush=True)
+
+
+def test_fast_path_declines_what_is_not_a_tensor(fast):
+    """None (fp8 kv rows come without k_rope) or any other non-tensor goes to
+    the Python path, which takes the fp8 call and raises for the rest."""
+    base = _case(6, 2, 3, 16, 256, 128)
+    dsa_amd.forward(*base)
+    torch.cuda.synchronize()
+    for i, bad in ((3, None), (4, base[4].tolist()), (0, 1.5), (1, "kv")):
+        args = list(base)
+        args[i] = bad
+        assert fast.forward(*args) is None, (i, type(bad))
+    # an fp8 call: the Python path, equal to the bf16 call on the dequantized rows
+    from oracle import dsa_oracle as O
+    rows = dsa_amd.quantize_kv_fp8(base[1], base[3])
+    kv_deq, rope = O.dequant_fp8_rows(rows)
+    got = dsa_amd.forward(base[0], rows, base[2], None, base[4])
+    want = dsa_amd.forward(base[0], kv_deq.cuda(), base[2], rope.cuda(), base[4],
+                           config=dsa_amd.plan_call((2, 3, 16, 256, 128), None, A._device_cus(base[0].device),
+                                                    kv_fp8=True)[0])
+    torch.cuda.synchronize()
+    for a, b in zip(got, want):
+        assert torch.equal(a, b)
