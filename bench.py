@@ -143,6 +143,12 @@ class Call:
             if self.opts is None:
                 self.opts = _lib.DsaFwdOptions()
             self.opts.arrivals = self.counters.data_ptr()
+        # Prefill-sized calls partition each token's indices by kv row range
+        # first, as forward() does: full() runs the bucketing into this
+        # buffer, main() reads it.
+        self.bucket = dsa_amd.api.buckets_rows(self.shape)
+        if self.bucket:
+            self.order = dsa_amd.bucket_indices(data[4], self.shape[3])
         self.out = torch.empty_like(q)
         self.mx = torch.empty((b, 1, sq, h), device=dev, dtype=torch.float32)
         self.sm = torch.empty_like(self.mx)
@@ -153,7 +159,8 @@ class Call:
         else:
             self.po = self.pm = self.pl = None
         p = lambda t: None if t is None else ctypes.c_void_p(t.data_ptr())  # noqa: E731
-        self.args = [p(t) for t in data] + [p(self.out), p(self.mx), p(self.sm), p(self.po), p(self.pm), p(self.pl)]
+        ins = list(data[:4]) + [self.order if self.bucket else data[4]]
+        self.args = [p(t) for t in ins] + [p(self.out), p(self.mx), p(self.sm), p(self.po), p(self.pm), p(self.pl)]
         self.lib = _lib.load()
         # W_UV projection after the attention: each call has its own weights
         # (one layer's [H, dv, 512]), so rotating calls do not share them.
@@ -166,15 +173,20 @@ class Call:
             self.uv_args = (p(self.w), uv_dim * 512, p(self.out_v))
 
     def full(self, stream):
-        """One whole call as ``dsa_amd.forward`` enqueues it: dsa_fwd (or
-        dsa_fwd_opts) -- the main kernel and its merge in one C call -- or,
-        with the W_UV projection, the main kernel and the merge + W_UV
-        launch."""
+        """One whole call as ``dsa_amd.forward`` enqueues it: for 256 tokens
+        or more the row bucketing of the indices, then dsa_fwd (or dsa_fwd_opts)
+        -- the main kernel and its merge in one C call -- or, with the W_UV
+        projection, the main kernel and the merge + W_UV launch."""
+        b, sq, h, length, k = self.shape
+        if self.bucket:
+            rc = self.lib.dsa_bucket_indices(ctypes.c_void_p(self.data[4].data_ptr()), self.args[4], b * sq, k,
+                                             length, stream)
+            if rc:
+                _lib.check(rc, "dsa_bucket_indices")
         if self.uv:
             self.main(stream)
             self.merge(stream)
             return
-        b, sq, h, length, k = self.shape
         if self.opts is None:
             rc = self.lib.dsa_fwd(*self.args, b, sq, h, length, k, ctypes.byref(self.plan), stream)
         else:

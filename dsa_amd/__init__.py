@@ -6,12 +6,13 @@ standalone FP32 split merge), ``select`` (the plan for a shape) and the
 lightning indexer that produces the indices (``indexer``, ``indexer_logits``,
 ``indexer_topk``), the fp8 kv cache row writer (``quantize_kv_fp8``) and the
 W_UV output projection after the attention (``project_uv``, ``merge_uv``,
-``forward(w_uv=)``).
+``forward(w_uv=)``) and the row-range bucketing of prefill-sized calls'
+indices (``bucket_indices``).
 """
-from .api import forward, merge, merge_uv, plan_call, project_uv
+from .api import bucket_indices, forward, merge, merge_uv, plan_call, project_uv
 from .config import CASE_SHAPES, SELECTED, Tuning, select
 from .indexer import indexer, indexer_logits, indexer_topk
 from .kvcache import quantize_kv_fp8
 
-__all__ = ["forward", "merge", "merge_uv", "project_uv", "plan_call", "Tuning", "CASE_SHAPES", "SELECTED", "select",
-           "indexer", "indexer_logits", "indexer_topk", "quantize_kv_fp8"]
+__all__ = ["forward", "merge", "merge_uv", "project_uv", "plan_call", "bucket_indices", "Tuning", "CASE_SHAPES",
+           "SELECTED", "select", "indexer", "indexer_logits", "indexer_topk", "quantize_kv_fp8"]

@@ -72,6 +72,7 @@ SIGNATURES = {
     "dsa_fwd_noalloc": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32,
                                ctypes.POINTER(DsaFwdOptions), ctypes.POINTER(DsaPlan), _vp]),
     "dsa_merge": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _vp]),
+    "dsa_bucket_indices": (_i32, [_vp, _vp, _i32, _i32, _i32, _vp]),
     "dsa_project_uv": (_i32, [_vp, _vp, _i64, _vp, _i32, _i32, _i32, _vp]),
     "dsa_merge_uv": (_i32, [_vp, _vp, _vp, _vp, _i64, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _vp]),
     "dsa_indexer_logits": (_i32, [_vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _vp]),

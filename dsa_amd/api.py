@@ -144,6 +144,25 @@ def _uv_launch(tokens: int, heads: int, dv: int, merge: bool) -> Launch:
     return Launch("project_uv", heads * nchunk * dsplit, 256, 4 * tb * 1024)
 
 
+BUCKET_MIN_TOKENS = 256  # calls with this many tokens or more bucket each token's indices first
+BUCKET_MAX_TOPK = 4096   # the row bucketing's limit (dsa_bucket_indices)
+
+
+def buckets_rows(shape) -> bool:
+    """Whether a call of this (B, SQ, H, L, TOPK) partitions each token's
+    indices by kv row range before the main kernel (dsa_bucket_indices):
+    prefill-sized calls, whose workgroups then gather from the same row
+    ranges at the same time and share L2 lines.  Decode calls have too few
+    workgroups per kv row to gain and skip the extra launch."""
+    return shape[0] * shape[1] >= BUCKET_MIN_TOKENS and shape[4] <= BUCKET_MAX_TOPK
+
+
+def bucket_lds_bytes(topk: int) -> int:
+    """LDS of the bucketing kernel: 65 counts per 64-slot chunk, 65 bucket
+    bases and the assembled row, 4 bytes each."""
+    return 4 * (-(-topk // 64) * 65 + 65 + topk)
+
+
 def plan_call(shape, config=None, cores: int = 256, kv_fp8: bool = False, w_uv_dim: int | None = None):
     """Plan of one call: (Tuning, partial-buffer shapes or None, launches).
 
@@ -178,6 +197,8 @@ def plan_call(shape, config=None, cores: int = 256, kv_fp8: bool = False, w_uv_d
         threads, lds = 64 * (config.bm // 16 + 6), _xs_lds_bytes(config.bm)
     launches = [Launch(f"sparse_mla_fwd_{variant}_h{config.bm}_kw{config.kv_waves}_bn{config.bn}_s{config.stages}",
                        tokens * config.split * (heads // config.bm), threads, lds)]
+    if buckets_rows(shape):
+        launches.insert(0, Launch("bucket_rows", tokens, 256, bucket_lds_bytes(shape[4])))
     partials = None
     merged = False
     if config.split > 1:
@@ -304,6 +325,13 @@ def forward(q, kv, q_rope, k_rope, indices, *, config=None, cores=None, return_k
     calls (only the plan of each shape, and the arrival counters below), and
     the call does not synchronise.
 
+    Calls of 256 tokens or more (TOPK up to 4096) first partition each
+    token's indices by kv row range into a fresh buffer
+    (``dsa_bucket_indices``, :func:`bucket_indices`; the caller's tensor is
+    not touched): the attention does not depend on the slots' order, and
+    with every token's tiles drawn from the same row ranges the workgroups
+    share L2 lines.
+
     Beyond the reference: ``scale`` (positive float) replaces the fixed 1/24,
     and ``block_table`` (int32 ``[B, max_blocks]``) selects paged kv, with kv
     and k_rope given as block pools ``[num_blocks, block_size, 1, 512 / 64]``;
@@ -353,8 +381,9 @@ def forward(q, kv, q_rope, k_rope, indices, *, config=None, cores=None, return_k
                                                                  None if uv is None else uv[0])
     if fused and arrivals is not None and arrivals.numel() < groups:
         raise ValueError(f"arrivals holds {arrivals.numel()} counters; this call needs {groups}")
+    bucket = buckets_rows(shape)
     if (default_plan and cores == _device_cus(device) and not fused and not fp8 and scale is None
-            and block_table is None and uv is None):
+            and block_table is None and uv is None and not bucket):
         _register_fast(device, shape, plan, partials)
 
     output = torch.empty_like(q)
@@ -371,11 +400,19 @@ def forward(q, kv, q_rope, k_rope, indices, *, config=None, cores=None, return_k
         part_l = part_o + partials[4]
 
     stream = torch._C._cuda_getCurrentRawStream(device.index)
+    lib = _lib.load()
+    idx_ptr = indices.data_ptr()
+    if bucket:
+        order = torch.empty_like(indices)
+        with _on_device(device):
+            rc = lib.dsa_bucket_indices(idx_ptr, order.data_ptr(), batch * queries, topk, length, stream)
+        if rc:
+            _lib.check(rc, "dsa_bucket_indices")
+        idx_ptr = order.data_ptr()
     args = (q.data_ptr(), kv.data_ptr(), q_rope.data_ptr(), None if k_rope is None else k_rope.data_ptr(),
-            indices.data_ptr(), output.data_ptr(), maximum.data_ptr(), denominator.data_ptr(),
+            idx_ptr, output.data_ptr(), maximum.data_ptr(), denominator.data_ptr(),
             part_o, part_m, part_l, batch, queries, heads, length, topk)
     merge_uv = uv is not None and config.split > 1
-    lib = _lib.load()
     with _on_device(device):
         if merge_uv:
             # Main kernel only; the merge runs inside the W_UV launch below.
@@ -534,6 +571,35 @@ def _on_device(device):
     if torch.cuda.current_device() == device.index:
         return _SAME_DEVICE
     return torch.cuda.device(device)
+
+
+def bucket_indices(indices, kv_len: int):
+    """Each token's indices stably partitioned by kv row range, as
+    ``forward`` orders them for prefill-sized calls (no reference
+    counterpart): bucket ``x >> s`` for a row index ``0 <= x < kv_len``
+    (``s`` the least shift with ``(kv_len - 1) >> s < 64``), then every
+    other entry (-1, out of range); within a bucket the caller's order.
+    ``indices [B,SQ,1,K]`` int32, contiguous, on a ROCm GPU, K <= 4096;
+    returns a new tensor of the same shape."""
+    if not isinstance(indices, torch.Tensor) or indices.dim() != 4 or indices.shape[2] != 1:
+        raise ValueError("indices must be [B,SQ,1,K]")
+    if isinstance(kv_len, bool) or not isinstance(kv_len, int) or not 0 < kv_len < 2 ** 31:
+        raise ValueError("kv_len must be a positive int below 2^31")
+    device = indices.device
+    if device.type != "cuda" or torch.version.hip is None or not indices.is_contiguous():
+        raise ValueError("indices must be contiguous on a ROCm GPU")
+    if indices.dtype != torch.int32:
+        raise ValueError("indices must be int32")
+    batch, queries, _, topk = indices.shape
+    if min(batch, queries, topk) <= 0 or topk > BUCKET_MAX_TOPK:
+        raise ValueError(f"indices must be non-empty with K <= {BUCKET_MAX_TOPK}")
+    out = torch.empty_like(indices)
+    stream = torch._C._cuda_getCurrentRawStream(device.index)
+    with _on_device(device):
+        rc = _lib.load().dsa_bucket_indices(indices.data_ptr(), out.data_ptr(), batch * queries, topk, kv_len,
+                                            stream)
+    _lib.check(rc, "dsa_bucket_indices")
+    return out
 
 
 def _check_partials(part_o, part_m, part_l):

@@ -21,7 +21,8 @@ ROOT = PKG.parent
 CSRC = PKG / "csrc"
 LIB = PKG / "libdsa_mi355x.so"
 OBJ_DIR = PKG / "_build"
-SOURCES = ["sparse_mla_fwd.hip", "merge.hip", "project_uv.hip", "indexer.hip", "fwd_scratch.hip", "abi.cpp"]
+SOURCES = ["sparse_mla_fwd.hip", "merge.hip", "project_uv.hip", "indexer.hip", "fwd_scratch.hip", "bucket_rows.hip",
+           "abi.cpp"]
 ARCH = "gfx950"
 ROCM_INCLUDE = Path(os.environ.get("ROCM_PATH", "/opt/rocm")) / "include"
 

@@ -52,7 +52,7 @@ int check_shape(int B, int SQ, int H, int L, int TOPK) {
 
 extern "C" {
 
-int dsa_version(void) { return (1 << 16) | 1; }
+int dsa_version(void) { return (1 << 16) | 2; }
 
 const char* dsa_last_error(void) { return g_err; }
 
@@ -233,6 +233,21 @@ int dsa_merge(const float* part_o, const float* part_m, const float* part_l, uin
         return fail(-1, "tokens, H, split must be positive (got %d, %d, %d)", tokens, H, split);
     const int rc = dsa::launch_merge(part_o, part_m, part_l, out, out_max, out_sum, tokens, H, split, stream);
     if (rc) return hip_fail(rc, "merge launch");
+    g_err[0] = 0;
+    return 0;
+}
+
+int dsa_bucket_indices(const int32_t* idx, int32_t* out, int tokens, int TOPK, int L, void* stream_) {
+    const hipStream_t stream = static_cast<hipStream_t>(stream_);
+    if (!idx || !out) return fail(-1, "NULL pointer argument");
+    if (tokens <= 0 || TOPK <= 0 || L <= 0)
+        return fail(-1, "tokens, TOPK and L must be positive (got %d, %d, %d)", tokens, TOPK, L);
+    if (TOPK > dsa::kBucketMaxTopk)
+        return fail(-1, "TOPK must be at most %d here (got %d)", dsa::kBucketMaxTopk, TOPK);
+    if (idx == out) return fail(-1, "out must not alias idx");
+    if (((uintptr_t)idx | (uintptr_t)out) & 3) return fail(-1, "idx and out must be 4-byte aligned");
+    const int rc = dsa::launch_bucket_rows(idx, out, tokens, TOPK, L, stream);
+    if (rc) return hip_fail(rc, "bucket launch");
     g_err[0] = 0;
     return 0;
 }

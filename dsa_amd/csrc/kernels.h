@@ -86,6 +86,18 @@ int64_t fwd_grid(const FwdParams& p);
 int launch_fwd(const FwdParams& p, int heads_per_group, int kv_waves, int tile_rows,
                int stages, int mfma, int pv_cols, hipStream_t stream);
 
+// Largest TOPK the row bucketing handles (its LDS holds one row).
+constexpr int kBucketMaxTopk = 4096;
+
+// Enqueue the row bucketing of `tokens` index rows of `topk` entries: each
+// row stably partitioned by x >> bucket_shift(kv_len) for 0 <= x < kv_len,
+// every other entry last; returns a hipError_t.  topk in [1, kBucketMaxTopk],
+// kv_len >= 1; out may not alias idx.
+int launch_bucket_rows(const int32_t* idx, int32_t* out, int64_t tokens, int topk, int kv_len, hipStream_t stream);
+
+// The least shift with (kv_len - 1) >> shift < 64.
+int bucket_shift(int kv_len);
+
 // Enqueue the split merge; returns a hipError_t.
 int launch_merge(const float* part_o, const float* part_m, const float* part_l,
                  uint16_t* out, float* out_max, float* out_sum,

@@ -98,7 +98,8 @@ typedef struct dsa_plan {
 } dsa_plan;
 
 /* Library version, (major << 16) | minor.  1.1: dsa_plan.pv_cols (a reserved
- * zero field in 1.0, which still selects the same plans) and dsa_fwd_noalloc. */
+ * zero field in 1.0, which still selects the same plans) and dsa_fwd_noalloc;
+ * 1.2: dsa_bucket_indices. */
 int dsa_version(void);
 
 /* Thread-local text of the last failure on this thread ("" if none). */
@@ -236,6 +237,26 @@ int dsa_fwd_main_opts(const uint16_t* q, const uint16_t* kv, const uint16_t* q_r
                       float* part_o, float* part_m, float* part_l,
                       int B, int SQ, int H, int L, int TOPK,
                       const dsa_fwd_options* opts, const dsa_plan* plan, void* stream);
+
+/*
+ * Row bucketing of the top-k indices, a pre-pass for prefill-sized calls.
+ * No counterpart in the reference (which takes the slots in the caller's
+ * order).
+ *
+ * out[t, :] (t < tokens, TOPK int32 entries each) is idx[t, :] stably
+ * partitioned by kv row range: bucket x >> s for a row index 0 <= x < L,
+ * where s is the least shift with (L - 1) >> s < 64, and one last bucket
+ * for every other entry (-1 or out of range); buckets ascending, and within
+ * a bucket the entries keep their order in idx.  A forward call on `out`
+ * instead of `idx` computes the same attention (the slots' order does not
+ * enter it) up to the order of its FP32 sums, and with many tokens it
+ * gathers faster: the kernels gather a token's slots 64 at a time, and with
+ * every token's tiles drawn from the same row ranges in the same order,
+ * workgroups that run together share L2 lines.  dsa_amd.forward runs it for
+ * calls of 256 tokens or more.  TOPK <= 4096; out must not alias idx.
+ * Launches one kernel on `stream`; allocates nothing.
+ */
+int dsa_bucket_indices(const int32_t* idx, int32_t* out, int tokens, int TOPK, int L, void* stream);
 
 /*
  * dsa_fwd_opts for callers that cannot allocate: code under HIP graph

@@ -40,6 +40,13 @@ Functions and the reference code each one restates:
                          the selection keeps the TOPK largest (ties: lower s)
                          in ascending s, -1 padded.
 
+* ``bucket_shift`` / ``bucket_rows_ref`` -- the row-range bucketing of
+                         prefill calls' indices (no reference counterpart:
+                         the reference takes the slots in the caller's order,
+                         dsa/workspace.py:76-141): a stable partition by
+                         x >> shift (shift the least with (L - 1) >> shift
+                         < 64), entries outside [0, L) last.
+
 * ``project_uv_ref``  -- the W_UV output projection after the attention (no
                          reference counterpart: the reference stops at the
                          latent output, README.md:81-83): DeepSeek-V3.2-Exp
@@ -63,6 +70,10 @@ before the scale) rejected.
 W_UV: an FP64 triple-loop brute force, one-hot weight rows (the projection
 then gathers latent columns exactly) and linearity, with planted mistakes
 (weights of the wrong head, the transposed head matrix) rejected.
+Bucketing: the shift's closed form at the 64-bucket boundaries, a
+distribution into 65 lists restatement, permutation / non-decreasing-key /
+stability properties, with planted mistakes (an unstable order, a sort by
+value, masked entries first) rejected.
 Indexer: FP64 brute-force logits (planted: ReLU or head weights dropped),
 brute-force selection over tie-heavy rows, -0.0 / +0.0, -inf and short rows
 (planted: ties taken from the top), and the float-key order.
@@ -209,6 +220,25 @@ def project_uv_ref(output, w_uv):
     xs = x.reshape(-1, heads, x.shape[-1]).transpose(0, 1)   # [H, T, 512]
     out = torch.bmm(xs, w.transpose(1, 2))                    # [H, T, dv], FP64 on the CPU
     return out.transpose(0, 1).reshape(*x.shape[:-1], w.shape[1])
+
+
+def bucket_shift(kv_len: int) -> int:
+    """The least shift with (kv_len - 1) >> shift < 64."""
+    shift = 0
+    while (kv_len - 1) >> shift >= 64:
+        shift += 1
+    return shift
+
+
+def bucket_rows_ref(indices, kv_len: int):
+    """``indices [..., K]`` int32 with each row stably ordered by bucket:
+    ``x >> bucket_shift(kv_len)`` for ``0 <= x < kv_len``, 64 for any other
+    entry."""
+    ids = np.ascontiguousarray(indices.cpu().numpy())
+    valid = (ids >= 0) & (ids < kv_len)
+    keys = np.where(valid, ids.astype(np.int64) >> bucket_shift(kv_len), 64)
+    order = np.argsort(keys, axis=-1, kind="stable")
+    return torch.from_numpy(np.take_along_axis(ids, order, axis=-1))
 
 
 def float_key(values):

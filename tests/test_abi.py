@@ -24,7 +24,7 @@ def test_header_declares_the_expected_entry_points():
         ["dsa_version", "dsa_last_error", "dsa_plan_for", "dsa_plan_check", "dsa_partial_elems",
          "dsa_fwd", "dsa_fwd_main", "dsa_fwd_opts", "dsa_fwd_main_opts", "dsa_plan_for_opts", "dsa_merge",
          "dsa_indexer_logits", "dsa_indexer_topk", "dsa_indexer_topk_ws_bytes", "dsa_indexer_topk_ws",
-         "dsa_project_uv", "dsa_merge_uv", "dsa_fwd_noalloc"])
+         "dsa_project_uv", "dsa_merge_uv", "dsa_fwd_noalloc", "dsa_bucket_indices"])
 
 
 def test_library_exports_every_declared_symbol():
@@ -36,8 +36,8 @@ def test_library_exports_every_declared_symbol():
 
 def test_version_and_last_error():
     lib = _lib.load()
-    # 1.1: dsa_plan.pv_cols and dsa_fwd_noalloc
-    assert lib.dsa_version() == (1 << 16) | 1
+    # 1.1: dsa_plan.pv_cols and dsa_fwd_noalloc; 1.2: dsa_bucket_indices
+    assert lib.dsa_version() == (1 << 16) | 2
     assert isinstance(lib.dsa_last_error(), bytes)
 
 

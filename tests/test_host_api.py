@@ -158,10 +158,24 @@ def test_plan_call_allocations_and_launches():
     _, _, launches = plan_call(shape, config=Tuning(16, 32, 4, kv_waves=2, stages=4, mfma=16, pv_cols=128), cores=256)
     assert launches[0].name.startswith("sparse_mla_fwd_xs_h16") and launches[0].block == 448
     config, partials, launches = plan_call(CASE_SHAPES["c5_prefill_h128"], cores=256)
-    assert config.split == 1 and partials is None and len(launches) == 1
-    # 128 heads, column-split PV: the eight-wave ping-pong kernel
-    assert launches[0].name.startswith("sparse_mla_fwd_pp") and launches[0].block == 512
-    assert launches[0].lds_bytes == 160 * 1024
+    assert config.split == 1 and partials is None and [l.name for l in launches][0] == "bucket_rows"
+    # 128 heads, column-split PV: the eight-wave ping-pong kernel after the row bucketing
+    assert len(launches) == 2 and launches[1].name.startswith("sparse_mla_fwd_pp") and launches[1].block == 512
+    assert launches[1].lds_bytes == 160 * 1024
+
+
+def test_prefill_calls_bucket_their_rows_first():
+    from dsa_amd import api as A
+    # 256 tokens or more, TOPK up to 4096: a row bucketing before the main kernel
+    assert A.buckets_rows(CASE_SHAPES["c4_prefill_h16"]) and A.buckets_rows(CASE_SHAPES["c5_prefill_h128"])
+    assert not A.buckets_rows(CASE_SHAPES["c2_decode_b8"]) and not A.buckets_rows(CASE_SHAPES["c3_decode_h16_mtp"])
+    assert not A.buckets_rows((1, 4096, 16, 8192, 8192)) and A.buckets_rows((2, 128, 16, 8192, 4096))
+    _, _, launches = plan_call(CASE_SHAPES["c4_prefill_h16"], cores=256)
+    # 32 chunks x 65 counts, 65 bases, the 2048-entry row
+    assert launches[0] == A.Launch("bucket_rows", 4096, 256, 4 * (32 * 65 + 65 + 2048)) and len(launches) == 2
+    assert A.bucket_lds_bytes(4096) == 4 * (64 * 65 + 65 + 4096) and A.bucket_lds_bytes(1) == 4 * (65 + 65 + 1)
+    _, _, launches = plan_call(CASE_SHAPES["c2_decode_b8"], cores=256)
+    assert all(l.name != "bucket_rows" for l in launches)
 
 
 def test_plan_call_fused_merge_is_one_launch():
@@ -369,10 +383,9 @@ def test_plan_call_w_uv_launches():
                                  w_uv_dim=128)
     assert [l.name for l in launches][1:] == ["merge_uv"]
     _, _, launches = A.plan_call((1, 4096, 128, 32768, 2048), Tuning(128, 32, 1, stages=4), w_uv_dim=128)
-    assert [l.name for l in launches][1:] == ["project_uv"]
+    assert [l.name for l in launches][0] == "bucket_rows" and [l.name for l in launches][2:] == ["project_uv"]
     # prefill: two chunks of 2048 tokens per head, 32-token tiles in four LDS buffers
-    _, _, launches = A.plan_call((1, 4096, 128, 32768, 2048), Tuning(128, 32, 1, stages=4), w_uv_dim=128)
-    assert launches[1].grid == 128 * 2 and launches[1].lds_bytes == 4 * 32 * 1024
+    assert launches[2].grid == 128 * 2 and launches[2].lds_bytes == 4 * 32 * 1024
     _, _, launches = A.plan_call((1, 4096, 16, 8192, 2048), None, w_uv_dim=128)
     assert launches[-1].grid == 16 * 16
     # 128 tokens, 256-wide values, split plan: 8 blocks of 16 tokens, d split in 2

@@ -21,7 +21,7 @@ from dsa_amd import api as A
 ALLOCATORS = ("empty", "empty_like", "empty_strided", "zeros", "zeros_like", "ones", "ones_like", "full",
               "full_like", "tensor", "randn")
 ENQUEUING = ("dsa_fwd", "dsa_fwd_main", "dsa_fwd_opts", "dsa_fwd_main_opts", "dsa_merge", "dsa_merge_uv",
-             "dsa_project_uv", "dsa_indexer_logits", "dsa_indexer_topk", "dsa_indexer_topk_ws")
+             "dsa_project_uv", "dsa_indexer_logits", "dsa_indexer_topk", "dsa_indexer_topk_ws", "dsa_bucket_indices")
 
 
 class TorchSpy:

@@ -543,3 +543,75 @@ def test_row_metric_skips_rows_the_oracle_left_out():
     acc = O.accuracy(act, exp)
     assert acc["rows"] == 1
     assert acc["max_row_normalized"] == pytest.approx(0.01, rel=1e-5)
+
+
+# ------------------------------------------------------- row-range bucketing
+
+
+def _bucket_lists(row, kv_len, shift):
+    """Distribution into 65 lists in the row's order, then concatenation."""
+    lists = [[] for _ in range(65)]
+    for x in row:
+        lists[x >> shift if 0 <= x < kv_len else 64].append(x)
+    return [x for lst in lists for x in lst]
+
+
+def _bucket_checks(fn, ids, kv_len):
+    got = fn(ids, kv_len).numpy()
+    shift = O.bucket_shift(kv_len)
+    src = ids.numpy().reshape(-1, ids.shape[-1])
+    for row, out in zip(src, got.reshape(src.shape)):
+        assert list(out) == _bucket_lists(list(row), kv_len, shift)
+        assert sorted(out) == sorted(row)  # a permutation of the row
+        keys = np.where((out >= 0) & (out < kv_len), out >> shift, 64)
+        assert (np.diff(keys) >= 0).all()
+
+
+def test_bucket_shift_closed_form():
+    # 64 buckets at most: (L - 1) >> shift < 64, and shift - 1 would not do
+    for kv_len, shift in ((1, 0), (64, 0), (65, 1), (128, 1), (129, 2), (5000, 7), (8192, 7), (8193, 8),
+                          (32768, 9), (65536, 10), (2 ** 31 - 1, 25)):
+        assert O.bucket_shift(kv_len) == shift
+        assert (kv_len - 1) >> shift < 64 and (shift == 0 or (kv_len - 1) >> (shift - 1) >= 64)
+
+
+@pytest.mark.parametrize("kv_len,K", [(1, 5), (64, 70), (5000, 300), (8192, 2048), (100000, 4096)])
+def test_bucket_rows_ref(kv_len, K):
+    g = torch.Generator().manual_seed(kv_len + K)
+    ids = torch.randint(0, kv_len, (2, 3, 1, K), generator=g, dtype=torch.int32)
+    u = torch.rand(ids.shape, generator=g)
+    ids[u < 0.1] = -1
+    ids[(u >= 0.1) & (u < 0.15)] = kv_len + 3
+    ids[(u >= 0.15) & (u < 0.17)] = -(2 ** 31)
+    _bucket_checks(O.bucket_rows_ref, ids, kv_len)
+    # stability: within a bucket the caller's order (tagged distinct values)
+    row = torch.randperm(kv_len if kv_len >= K else K, generator=g)[:K].int() % kv_len
+    out = O.bucket_rows_ref(row.view(1, 1, 1, K), kv_len).view(-1).tolist()
+    pos = {v: i for i, v in reversed(list(enumerate(row.tolist())))}
+    shift = O.bucket_shift(kv_len)
+    for a, b in zip(out, out[1:]):
+        if a >> shift == b >> shift and a != b:
+            assert pos[a] < pos[b]
+
+
+def test_bucket_planted_mistakes_are_caught():
+    g = torch.Generator().manual_seed(7)
+    kv_len = 8192
+    ids = torch.randint(0, kv_len, (1, 2, 1, 512), generator=g, dtype=torch.int32)
+    ids[torch.rand(ids.shape, generator=g) < 0.2] = -1
+
+    def unstable(x, n):  # buckets in order, rows reversed inside each
+        return O.bucket_rows_ref(x.flip(-1).contiguous(), n)
+
+    def by_value(x, n):  # a full unsigned sort: same buckets, other order inside
+        key = (x.long() & 0xFFFFFFFF).sort(dim=-1).values
+        return torch.where(key < 2 ** 31, key, key - 2 ** 32).int()
+
+    def masked_first(x, n):
+        return torch.from_numpy(np.ascontiguousarray(np.take_along_axis(
+            x.numpy(), np.argsort(np.where((x.numpy() >= 0) & (x.numpy() < n),
+                                           x.numpy().astype(np.int64) >> 7, -1), axis=-1, kind="stable"), axis=-1)))
+
+    for planted in (unstable, by_value, masked_first):
+        with pytest.raises(AssertionError):
+            _bucket_checks(planted, ids, kv_len)
