@@ -5,7 +5,9 @@ hipMemsetAsync, and the in-kernel merge leaves its arrival counters at zero
 after every call, so a captured call must replay exactly: every replay is
 compared bit for bit with the eager result, with the program's own eager
 calls and synchronisations between the replays, and the inputs are changed
-in place between replays to show that the graph reads them afresh.
+in place between replays to show that the graph reads them afresh.  Calls of
+256 tokens or more also run the row bucketing, into an index buffer that
+forward() allocates (from the graph's private pool under capture).
 """
 import pytest
 import torch
@@ -44,6 +46,11 @@ CASES = [  # (B, SQ, H), plan, W_UV value dim (0: none)
     ((8, 1, 128), Tuning(32, 32, 8, kv_waves=2, stages=4, mfma=16, pv_cols=128), 0),     # specialised waves + merge
     ((2, 1, 128), Tuning(32, 64, 4, kv_waves=2, mfma=16), 128),                   # main + merge_uv
     ((2, 3, 16), Tuning(16, 64, 1, kv_waves=4, mfma=16), 128),                    # main + project_uv
+    # 256 tokens or more: the row bucketing runs first, into a buffer the
+    # capture allocates from the graph's pool
+    ((1, 260, 16), Tuning(16, 64, 1, kv_waves=4, mfma=16, pv_cols=128), 0),      # bucketing + column-split
+    ((2, 130, 128), Tuning(128, 32, 1, kv_waves=1, stages=4, mfma=16, pv_cols=128), 0),  # bucketing + ping-pong
+    ((1, 256, 16), Tuning(16, 64, 1, kv_waves=4, mfma=16, pv_cols=128), 128),    # bucketing + project_uv
 ]
 
 
