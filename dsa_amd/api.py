@@ -539,7 +539,9 @@ def _fast_path():
                 spec = importlib.util.spec_from_file_location("dsa_amd._fast", path)
                 module = importlib.util.module_from_spec(spec)
                 spec.loader.exec_module(module)
-                module.set_entry(ctypes.cast(_lib.load().dsa_fwd, ctypes.c_void_p).value)
+                lib = _lib.load()
+                module.set_entry(*(ctypes.cast(f, ctypes.c_void_p).value
+                                   for f in (lib.dsa_fwd, lib.dsa_fwd_main, lib.dsa_merge)))
             _fast_state.append(module)
     return _fast_state[0]
 

@@ -23,11 +23,14 @@
 
 namespace {
 
-// int dsa_fwd(q, kv, q_rope, k_rope, idx, out, out_max, out_sum, part_o,
-//             part_m, part_l, B, SQ, H, L, TOPK, const dsa_plan*, void* stream)
+// int dsa_fwd / dsa_fwd_main(q, kv, q_rope, k_rope, idx, out, out_max,
+//     out_sum, part_o, part_m, part_l, B, SQ, H, L, TOPK, const dsa_plan*, void* stream)
 using FwdFn = int (*)(const void*, const void*, const void*, const void*, const void*, void*, void*, void*, void*,
                       void*, void*, int, int, int, int, int, const void*, void*);
-FwdFn g_fwd = nullptr;
+// int dsa_merge(part_o, part_m, part_l, out, out_max, out_sum, tokens, H, split, void* stream)
+using MergeFn = int (*)(const void*, const void*, const void*, void*, void*, void*, int, int, int, void*);
+FwdFn g_fwd = nullptr, g_fwd_main = nullptr;
+MergeFn g_merge = nullptr;
 
 struct Entry {
     std::array<int32_t, 8> plan;  // the fields of struct dsa_plan, in order
@@ -71,7 +74,7 @@ py::object forward(py::handle hq, py::handle hkv, py::handle hqr, py::handle hkr
     const at::Tensor& q_rope = THPVariable_Unpack(hqr.ptr());
     const at::Tensor& k_rope = THPVariable_Unpack(hkr.ptr());
     const at::Tensor& idx = THPVariable_Unpack(hidx.ptr());
-    if (g_fwd == nullptr || q.dim() != 4 || kv.dim() != 4 || idx.dim() != 4) return py::none();
+    if (g_fwd == nullptr || g_fwd_main == nullptr || g_merge == nullptr || q.dim() != 4 || kv.dim() != 4 || idx.dim() != 4) return py::none();
     const int64_t B = q.size(0), SQ = q.size(1), H = q.size(2), L = kv.size(1), K = idx.size(3);
     if (q.size(3) != 512 || !dims(kv, {B, L, 1, 512}) || !dims(q_rope, {B, SQ, H, 64}) ||
         !dims(k_rope, {B, L, 1, 64}) || !dims(idx, {B, SQ, 1, K}))
@@ -96,25 +99,44 @@ py::object forward(py::handle hq, py::handle hkv, py::handle hqr, py::handle hkr
         e = it->second;
     }
     c10::DeviceGuard guard(dev);
-    at::Tensor out = at::empty_like(q);
-    at::Tensor mx = at::empty({B, 1, SQ, H}, q.options().dtype(at::kFloat));
-    at::Tensor sm = at::empty_like(mx);
-    at::Tensor part;
-    char* pbase = nullptr;
-    if (e.part_floats > 0) {
-        part = at::empty({e.part_floats}, q.options().dtype(at::kFloat));
-        pbase = static_cast<char*>(part.data_ptr());
-    }
     void* stream = c10::hip::getCurrentHIPStream(dev.index()).stream();
+    const auto f32 = q.options().dtype(at::kFloat);
+    if (e.part_floats > 0) {
+        // A split plan: the main kernel writes only the partials, so it is
+        // launched before the outputs are allocated (their allocation then
+        // overlaps the kernel), and the merge kernel follows -- the two
+        // launches dsa_fwd makes, in the same order on the same stream.
+        at::Tensor part = at::empty({e.part_floats}, f32);
+        char* pbase = static_cast<char*>(part.data_ptr());
+        const float* pm = reinterpret_cast<const float*>(pbase + e.off_m);
+        const float* pl = reinterpret_cast<const float*>(pbase + e.off_l);
+        int rc = g_fwd_main(q.data_ptr(), kv.data_ptr(), q_rope.data_ptr(), k_rope.data_ptr(), idx.data_ptr(),
+                            nullptr, nullptr, nullptr, pbase, pbase + e.off_m, pbase + e.off_l, (int)B, (int)SQ,
+                            (int)H, (int)L, (int)K, e.plan.data(), stream);
+        if (rc != 0) return py::int_(rc);
+        at::Tensor out = at::empty_like(q);
+        at::Tensor mx = at::empty({B, 1, SQ, H}, f32);
+        at::Tensor sm = at::empty_like(mx);
+        rc = g_merge(pbase, pm, pl, out.data_ptr(), mx.data_ptr(), sm.data_ptr(), (int)(B * SQ), (int)H,
+                     e.plan[2], stream);
+        if (rc != 0) return py::int_(rc);
+        return py::make_tuple(out, mx, sm);
+    }
+    at::Tensor out = at::empty_like(q);
+    at::Tensor mx = at::empty({B, 1, SQ, H}, f32);
+    at::Tensor sm = at::empty_like(mx);
     const int rc = g_fwd(q.data_ptr(), kv.data_ptr(), q_rope.data_ptr(), k_rope.data_ptr(), idx.data_ptr(),
-                         out.data_ptr(), mx.data_ptr(), sm.data_ptr(), pbase, pbase ? pbase + e.off_m : nullptr,
-                         pbase ? pbase + e.off_l : nullptr, (int)B, (int)SQ, (int)H, (int)L, (int)K, e.plan.data(),
-                         stream);
+                         out.data_ptr(), mx.data_ptr(), sm.data_ptr(), nullptr, nullptr, nullptr, (int)B, (int)SQ,
+                         (int)H, (int)L, (int)K, e.plan.data(), stream);
     if (rc != 0) return py::int_(rc);
     return py::make_tuple(out, mx, sm);
 }
 
-void set_entry(uint64_t dsa_fwd_address) { g_fwd = reinterpret_cast<FwdFn>(dsa_fwd_address); }
+void set_entry(uint64_t dsa_fwd_address, uint64_t dsa_fwd_main_address, uint64_t dsa_merge_address) {
+    g_fwd = reinterpret_cast<FwdFn>(dsa_fwd_address);
+    g_fwd_main = reinterpret_cast<FwdFn>(dsa_fwd_main_address);
+    g_merge = reinterpret_cast<MergeFn>(dsa_merge_address);
+}
 
 void register_plan(int64_t dev, int64_t B, int64_t SQ, int64_t H, int64_t L, int64_t K, std::vector<int32_t> plan,
                    int64_t part_floats, int64_t off_m, int64_t off_l) {
@@ -138,7 +160,7 @@ void clear_plans() {
 
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
     m.def("forward", &forward, "dsa_amd.forward for a planned shape, or None");
-    m.def("set_entry", &set_entry, "address of the library's dsa_fwd");
+    m.def("set_entry", &set_entry, "addresses of the library's dsa_fwd, dsa_fwd_main and dsa_merge");
     m.def("register_plan", &register_plan, "plan of a (device, B, SQ, H, L, TOPK) call");
     m.def("clear_plans", &clear_plans, "forget every registered plan");
 }
