@@ -99,6 +99,24 @@ def test_paged_equals_contiguous_bitwise(config, block_size):
     _check(f"paged bs={block_size}", *paged, O.reference(q, kv, qr, kr, ids))
 
 
+@pytest.mark.parametrize("H,config", [(16, None), (128, None), (16, Tuning(16, 64, 1, kv_waves=4, mfma=16))],
+                         ids=str)
+def test_paged_prefill_bucketed_equals_contiguous(H, config):
+    """260 tokens: forward buckets each token's indices by logical row range
+    first (the same order for the paged and the contiguous call, which then
+    agree bit for bit)."""
+    q, kv, qr, kr, ids = _case(12, B=1, SQ=260, H=H, L=4096, K=700)
+    kv_pool, kr_pool, table = _paged(kv, kr, 64, seed=13)
+    dev = [t.cuda() for t in (q, kv, qr, kr, ids, kv_pool, kr_pool, table)]
+    print(f"[paged prefill H={H} {config}] launching", flush=True)
+    contiguous = dsa_amd.forward(dev[0], dev[1], dev[2], dev[3], dev[4], config=config)
+    paged = dsa_amd.forward(dev[0], dev[5], dev[2], dev[6], dev[4], config=config, block_table=dev[7])
+    torch.cuda.synchronize()
+    for a, b in zip(contiguous, paged):
+        assert torch.equal(a, b)
+    _check(f"paged prefill H={H}", *paged, O.reference(q, kv, qr, kr, ids))
+
+
 @pytest.mark.parametrize("config", [None, Tuning(16, 64, 3, kv_waves=4, mfma=16)], ids=str)
 def test_paged_holes_are_masked(config):
     q, kv, qr, kr, ids = _case(4)
