@@ -2383,7 +2383,6 @@ __global__ __launch_bounds__(kPPThreads, 1) void sparse_mla_fwd_pp(FwdParams p) 
         // raised wave priority over the other group's PV.
         __builtin_amdgcn_s_setprio(2);
         f32x4 sacc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
-        i32x4 ivs[2];  // slot indices of the lane's score rows, read late in the chain
         bf16x8 kf[KD];
 #pragma unroll
         for (int j = 0; j < KD; ++j) kf[j] = kfrag(j);
@@ -2391,22 +2390,28 @@ __global__ __launch_bounds__(kPPThreads, 1) void sparse_mla_fwd_pp(FwdParams p) 
         for (int step = 0; step < 36; ++step) {
             sacc[step & 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[step % KD], qf[step >> 1], sacc[step & 1], 0, 0, 0);
             if (step + KD < 36) kf[step % KD] = kfrag(step + KD);
-            if (step == 30)
-#pragma unroll
-                for (int sub = 0; sub < 2; ++sub)
-                    ivs[sub] = lds_load<i32x4>(idx_lds + 4 * (t * BN + 16 * sub + 4 * lg));
             __builtin_amdgcn_sched_barrier(0);
         }
         __builtin_amdgcn_s_setprio(0);
-        // Lane holds rows 16 s + 4 g + r of head n16.  Raw scores with masked
-        // rows at -inf; the scale folds into the max and one FMA per score.
+        // Lane holds rows 16 s + 4 g + r of head n16.  Raw scores; the
+        // compacted slots are all valid except the padding (-1) of the last
+        // tile, whose rows are masked at -inf.  The scale folds into the max
+        // and one FMA per score.
         float x[8];
+#pragma unroll
+        for (int r = 0; r < 8; ++r) x[r] = sacc[r >> 2][r & 3];
+        if (t == nt - 1) {
+#pragma unroll
+            for (int sub = 0; sub < 2; ++sub) {
+                const i32x4 iv = lds_load<i32x4>(idx_lds + 4 * (t * BN + 16 * sub + 4 * lg));
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    if (iv[r] < 0) x[4 * sub + r] = -INFINITY;
+            }
+        }
         float smax = -INFINITY;
 #pragma unroll
-        for (int r = 0; r < 8; ++r) {
-            x[r] = ivs[r >> 2][r & 3] < 0 ? -INFINITY : sacc[r >> 2][r & 3];
-            smax = fmaxf(smax, x[r]);
-        }
+        for (int r = 0; r < 8; ++r) smax = fmaxf(smax, x[r]);
         smax = max_xor32(max_xor16(smax));
         m_true = fmaxf(m_true, smax * p.score_scale_log2);
         if (m_ref == -FLT_MAX) m_ref = m_true;  // first valid rows: O and l are still zero
