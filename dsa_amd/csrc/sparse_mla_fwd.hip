@@ -966,6 +966,48 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t group_block(const FwdParams& p
 
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 
+// FP32 partial rows staged in LDS: row hl of the workgroup's heads at
+// stage + kPartRow * hl (the 16 extra bytes put the 16 rows that one
+// ds_write_b128 pass touches on distinct banks).
+//
+// A lane's accumulators hold 4 columns of one head per column block, so a
+// store straight from them writes sixteen 64-byte pieces of 16 head rows per
+// instruction, and the cost of the partial stores tracks those pieces, not
+// the bytes.  Staged in the (then free) ring and stored as whole 1 KiB
+// halves of a row, each instruction writes 8 full 128-byte lines: main
+// kernel C2 -0.8 us, C1 -0.4 us, C3 -1.3 us, outputs bit-identical.
+constexpr int kPartRow = 2048 + 16;
+enum PartStore { kPartPlain = 0, kPartNonTemporal = 1, kPartAgent = 2 };
+
+// Store of the workgroup's `heads` staged partial rows to part_o as whole
+// 1 KiB halves of a row (one instruction each), wave w of nwaves taking
+// halves w, w + nwaves, ...  Non-temporal for the partials only the merge
+// kernel reads (the specialised-wave kernel's: -0.8 us at C2 against plain
+// stores; level for the column-split kernel's), agent-coherent for the
+// in-kernel merge.
+template <int MODE>
+__device__ __forceinline__ void store_staged_partials(const FwdParams& p, const WgCoords& c, int head0, int heads,
+                                                      uint32_t stage, int wave, int nwaves, int lane) {
+    if constexpr (MODE == kPartAgent) {
+        const __amdgpu_buffer_rsrc_t rs = group_block(p, c.token, c.sp, head0, heads);
+        for (int i = wave; i < 2 * heads; i += nwaves) {
+            const u32x4 v = lds_load<u32x4>(stage + (uint32_t)((i >> 1) * kPartRow + 1024 * (i & 1) + 16 * lane));
+            __builtin_amdgcn_raw_buffer_store_b128(v, rs, (i >> 1) * 2048 + 1024 * (i & 1) + 16 * lane, 0,
+                                                   kAgentCoherent);
+        }
+    } else {
+        float* base = p.part_o + (((int64_t)c.token * p.nsplit + c.sp) * p.H + head0) * 512 + 4 * lane;
+        for (int i = wave; i < 2 * heads; i += nwaves) {
+            const f32x4 v = lds_load<f32x4>(stage + (uint32_t)((i >> 1) * kPartRow + 1024 * (i & 1) + 16 * lane));
+            f32x4* dst = reinterpret_cast<f32x4*>(base + (i >> 1) * 512 + 256 * (i & 1));
+            if constexpr (MODE == kPartNonTemporal)
+                __builtin_nontemporal_store(v, dst);
+            else
+                *dst = v;
+        }
+    }
+}
+
 // Count-in of a workgroup's partials (every wave calls it): true in the
 // workgroup that arrives last, which then owns the group's merge and has
 // zeroed the counter for the next call.
@@ -1726,14 +1768,24 @@ __global__ __launch_bounds__(PROD ? 2 * kThreads : kThreads, 1) void sparse_mla_
     // ---- epilogue: sum l and take the max over the four waves' rows (the ring
     // is free once every wave is past its last read).
     lds_barrier();
+    constexpr int kPartOff = 4096;  // staged partial rows, past the l / max exchange
+    static_assert(kPartOff + X::BM * kPartRow <= X::RING, "staged partials fit the ring");
     if (producer) {
-        // the compute waves' remaining barriers
+        // the compute waves' remaining barriers; the partial rows' stores
+        // are shared by all eight waves
         lds_barrier();
         if (p.nsplit == 1) {
             lds_barrier();
-        } else if (!(HB > 1 || p.arrivals == nullptr)) {
-            lds_barrier();
-            lds_barrier();
+        } else {
+            lds_barrier();  // rows staged
+            if (HB > 1 || p.arrivals == nullptr) {
+                store_staged_partials<kPartPlain>(p, c, head0, X::BM, lds + kPartOff, wave, 2 * kWaves, lane);
+            } else {
+                store_staged_partials<kPartAgent>(p, c, head0, X::BM, lds + kPartOff, wave, 2 * kWaves, lane);
+                wait_vmcnt<0>();  // the count-in's barriers (group_count_in)
+                lds_barrier();
+                lds_barrier();
+            }
         }
         return;
     }
@@ -1795,36 +1847,38 @@ __global__ __launch_bounds__(PROD ? 2 * kThreads : kThreads, 1) void sparse_mla_
         for (int hr = wave; hr < X::BM; hr += kWaves)
             *reinterpret_cast<bf16x8*>(obase + (int64_t)hr * 512) =
                 lds_load<bf16x8>(lds + STAGE_OFF + hr * HROW + 16 * eln);
-    } else if (HB > 1 || p.arrivals == nullptr) {
+    } else {
+        // FP32 partial rows staged past the l / max exchange, then stored as
+        // whole 1 KiB halves by every wave; with the in-kernel merge they and
+        // m / l are stored agent-coherent and the last workgroup of the
+        // (token, head group) merges.
 #pragma unroll
         for (int hb = 0; hb < HB; ++hb) {
             const int head = head0 + hb * 16 + en16;
             const float to_true = fast_exp2(m_ref[hb] - m_true[hb]);
-            const int64_t prow = ((int64_t)c.token * p.nsplit + c.sp) * p.H + head;
-            float* orow = p.part_o + prow * 512 + 128 * wave + 4 * eg;
+            const uint32_t srow = lds + kPartOff + (uint32_t)((hb * 16 + en16) * kPartRow + 4 * (128 * wave + 4 * eg));
 #pragma unroll
-            for (int cb = 0; cb < 8; ++cb) *reinterpret_cast<f32x4*>(orow + 16 * cb) = oacc[hb][cb] * to_true;
+            for (int cb = 0; cb < 8; ++cb) lds_store<f32x4>(srow + 64 * cb, oacc[hb][cb] * to_true);
             if (writes_ml) {
-                p.part_m[prow] = m_true[hb] * kLn2;
-                p.part_l[prow] = l_run[hb] * to_true;
+                const int64_t prow = ((int64_t)c.token * p.nsplit + c.sp) * p.H + head;
+                if (HB > 1 || p.arrivals == nullptr) {
+                    p.part_m[prow] = m_true[hb] * kLn2;
+                    p.part_l[prow] = l_run[hb] * to_true;
+                } else {
+                    __hip_atomic_store(p.part_m + prow, m_true[hb] * kLn2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    __hip_atomic_store(p.part_l + prow, l_run[hb] * to_true, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+                }
             }
         }
-    } else {
-        // In-kernel merge (one head block): the same partials, stored
-        // agent-coherent; the last workgroup of the (token, head group) merges.
-        const float to_true = fast_exp2(m_ref[0] - m_true[0]);
-        const __amdgpu_buffer_rsrc_t rs = group_block(p, c.token, c.sp, head0, 16);
-        const uint32_t voff = (uint32_t)(en16 * 2048 + 16 * eg + 64 * 8 * wave);
-#pragma unroll
-        for (int cb = 0; cb < 8; ++cb)
-            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, oacc[0][cb] * to_true), rs, voff + 64 * cb,
-                                                   0, kAgentCoherent);
-        if (writes_ml) {
-            const int64_t prow = ((int64_t)c.token * p.nsplit + c.sp) * p.H + head0 + en16;
-            __hip_atomic_store(p.part_m + prow, m_true[0] * kLn2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(p.part_l + prow, l_run[0] * to_true, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        lds_barrier();  // rows staged
+        constexpr int kStoreWaves = PROD ? 2 * kWaves : kWaves;
+        if (HB > 1 || p.arrivals == nullptr) {
+            store_staged_partials<kPartPlain>(p, c, head0, X::BM, lds + kPartOff, wave, kStoreWaves, eln);
+        } else {
+            store_staged_partials<kPartAgent>(p, c, head0, X::BM, lds + kPartOff, wave, kStoreWaves, eln);
+            merge_if_last<8>(p, c, head0, 16, en16, eg, writes_ml, 8 * wave, flag_lds);
         }
-        merge_if_last<8>(p, c, head0, 16, en16, eg, writes_ml, 8 * wave, flag_lds);
     }
 }
 
@@ -1997,7 +2051,14 @@ __global__ __launch_bounds__(64 * XsLds<HB>::WAVES, 1) void sparse_mla_fwd_xs(Fw
                     lds_load<bf16x8>(lds + hr * 1040 + 16 * lane);
             return false;
         }
-        if (HB > 1 || p.arrivals == nullptr) return false;
+        // FP32 partial rows staged in the ring, stored as whole 1 KiB halves
+        static_assert(BM * kPartRow <= X::IDX_OFF, "staged partials fit the ring");
+        lds_barrier();  // rows staged
+        if (HB > 1 || p.arrivals == nullptr) {
+            store_staged_partials<kPartNonTemporal>(p, c, head0, BM, lds, wave, X::WAVES, lane);
+            return false;
+        }
+        store_staged_partials<kPartAgent>(p, c, head0, BM, lds, wave, X::WAVES, lane);
         return group_count_in(p, c, flag_lds);
     };
 
@@ -2207,31 +2268,21 @@ __global__ __launch_bounds__(64 * XsLds<HB>::WAVES, 1) void sparse_mla_fwd_xs(Fw
                 p.out_max[(int64_t)c.token * p.H + head] = mt * kLn2;
                 p.out_sum[(int64_t)c.token * p.H + head] = l * fast_exp2(mr - mt);
             }
-        } else if (HB > 1 || p.arrivals == nullptr) {
-            const float to_true = fast_exp2(mr - mt);
-            const int64_t prow = ((int64_t)c.token * p.nsplit + c.sp) * p.H + head;
-            float* orow = p.part_o + prow * 512 + 256 * v + 4 * g;
-#pragma unroll
-            // Non-temporal: the partials are read once, by the merge kernel
-            // (C2: main kernel -1.1 us, call -0.4 us; the column-split
-            // kernel's partials gained nothing from it).
-            for (int cb = 0; cb < 16; ++cb)
-                __builtin_nontemporal_store(oacc[hb][cb] * to_true, reinterpret_cast<f32x4*>(orow + 16 * cb));
-            if (writes_ml) {
-                p.part_m[prow] = mt * kLn2;
-                p.part_l[prow] = l * to_true;
-            }
         } else {
-            // In-kernel merge: the same partials, stored agent-coherent for the
+            // FP32 rows staged in the ring (finish() stores them); with the
+            // in-kernel merge they and m / l are stored agent-coherent for the
             // group's last workgroup (merge_group_cols reads them back).
             const float to_true = fast_exp2(mr - mt);
-            const __amdgpu_buffer_rsrc_t rs = group_block(p, c.token, c.sp, head0, 16);
-            const uint32_t voff = (uint32_t)(n16 * 2048 + 16 * g + 64 * 16 * v);
+            const uint32_t srow = lds + (uint32_t)(hl * kPartRow + 4 * (256 * v + 4 * g));
 #pragma unroll
-            for (int cb = 0; cb < 16; ++cb)
-                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, oacc[hb][cb] * to_true), rs,
-                                                       voff + 64 * cb, 0, kAgentCoherent);
-            if (writes_ml) {
+            for (int cb = 0; cb < 16; ++cb) lds_store<f32x4>(srow + 64 * cb, oacc[hb][cb] * to_true);
+            if (HB > 1 || p.arrivals == nullptr) {
+                if (writes_ml) {
+                    const int64_t prow = ((int64_t)c.token * p.nsplit + c.sp) * p.H + head;
+                    p.part_m[prow] = mt * kLn2;
+                    p.part_l[prow] = l * to_true;
+                }
+            } else if (writes_ml) {
                 const int64_t prow = ((int64_t)c.token * p.nsplit + c.sp) * p.H + head;
                 __hip_atomic_store(p.part_m + prow, mt * kLn2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 __hip_atomic_store(p.part_l + prow, l * to_true, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
