@@ -169,6 +169,19 @@ __device__ __forceinline__ int sw_kv(int r) {
 }
 __device__ __forceinline__ int sw_rope(int r) { return (r >> 1) & 7; }
 
+// QK k-order of the specialised-wave and ping-pong kernels: k-step ks (32 of
+// the 512 latent dims) takes logical chunks 4 ks .. 4 ks + 3, lane group g
+// holding chunk 4 ks + qk_lane_chunk(g), so that one Q fragment load reads a
+// whole 64-byte piece of each of its 16 head rows (16 lines per instruction)
+// where chunk 16 g + ks reads 16 bytes of 64 lines.  The permutation
+// [0, 3, 1, 2] keeps the low two chunk bits of groups 0 and 1 (and of 2 and
+// 3) in the same class {0, 3} or {1, 2}, which is what keeps the K reads of
+// one ds_read_b128 pass on 16 distinct bank groups under sw_kv (with g in
+// place of qk_lane_chunk(g) a pass would meet 2-way conflicts).  Measured:
+// C2 -2.4 %, C5 -0.9 %; the column-split kernel (C4 +0.7 % with it) and the
+// narrow kernel keep chunk 16 g + ks.
+__device__ __forceinline__ int qk_lane_chunk(int g) { return (0x9C >> (2 * g)) & 3; }
+
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // Cross-lane reductions over lanes l and l ^ 32 (l ^ 16) with the gfx950
@@ -2014,14 +2027,14 @@ __global__ __launch_bounds__(64 * XsLds<HB>::WAVES, 1) void sparse_mla_fwd_xs(Fw
     // Indices masked and in LDS before the Q loads issue: deferring them
     // behind Q (as the other kernels do) measured 0.35 us slower at C2.
     if (wave < 4) store_indices<BN>(fetch_indices<BN>(p, c), idx_lds, p, c);
-    // Q of the QK wave's head block: lane holds Q[head][128 g + 8 ks .. + 7];
-    // ks 16, 17 from q_rope (dims 32 (ks - 16) + 8 g).
+    // Q of the QK wave's head block: lane holds Q[head][32 ks + 8 qk_lane_chunk(g)
+    // .. + 7]; ks 16, 17 from q_rope (dims 32 (ks - 16) + 8 g).
     bf16x8 qf[18];
     if (wave < HB) {
         const int head = head0 + 16 * wave + n16;
-        const uint16_t* qrow = p.q + ((int64_t)c.token * p.H + head) * 512 + 128 * g;
+        const uint16_t* qrow = p.q + ((int64_t)c.token * p.H + head) * 512 + 8 * qk_lane_chunk(g);
 #pragma unroll
-        for (int ks = 0; ks < 16; ++ks) qf[ks] = *reinterpret_cast<const bf16x8*>(qrow + 8 * ks);
+        for (int ks = 0; ks < 16; ++ks) qf[ks] = *reinterpret_cast<const bf16x8*>(qrow + 32 * ks);
         const uint16_t* rrow = p.q_rope + ((int64_t)c.token * p.H + head) * 64 + 8 * g;
         qf[16] = *reinterpret_cast<const bf16x8*>(rrow);
         qf[17] = *reinterpret_cast<const bf16x8*>(rrow + 32);
@@ -2120,13 +2133,15 @@ __global__ __launch_bounds__(64 * XsLds<HB>::WAVES, 1) void sparse_mla_fwd_xs(Fw
                 if (s == c.nt) break;
                 const uint32_t stage = X::stage(lds, s);
                 // K fragment of k-step ks, subtile sub: row 16 sub + n16, logical
-                // chunk 16 g + ks (kv) at byte 256 g + ((ks ^ sw_kv(n16)) << 4);
-                // rope chunk 4 (ks - 16) + g at ((4 (ks - 16) + g) ^ sw_rope(n16)) << 4.
-                const uint32_t kbase = (stage + n16 * 1024 + ((uint32_t)g << 8)) | ((uint32_t)sw_kv(n16) << 4);
+                // chunk 4 ks + qk_lane_chunk(g) (kv) at byte 256 (ks >> 2) +
+                // (((4 (ks & 3) + qk_lane_chunk(g)) ^ sw_kv(n16)) << 4); rope chunk
+                // 4 (ks - 16) + g at ((4 (ks - 16) + g) ^ sw_rope(n16)) << 4.
+                const uint32_t kbase = (stage + n16 * 1024) | ((uint32_t)(qk_lane_chunk(g) ^ sw_kv(n16)) << 4);
                 const uint32_t rbase = (stage + X::KV_BYTES + n16 * 128) | ((uint32_t)(g ^ sw_rope(n16)) << 4);
                 auto kfrag = [&](int st) -> bf16x8 {
                     const int ks = st >> 1, sub = st & 1;
-                    if (ks < 16) return lds_load<bf16x8>((kbase ^ (16u * ks)) + sub * 16 * 1024);
+                    if (ks < 16)
+                        return lds_load<bf16x8>((kbase ^ (64u * (ks & 3))) + 256u * (ks >> 2) + sub * 16 * 1024);
                     return lds_load<bf16x8>((rbase ^ (64u * (ks - 16))) + sub * 16 * 128);
                 };
                 constexpr int KD = XS_QK_DEPTH;
@@ -2380,14 +2395,14 @@ __global__ __launch_bounds__(kPPThreads, 1) void sparse_mla_fwd_pp(FwdParams p) 
     IdxRegs<> ids;
     if (wave < 4) ids = fetch_indices<BN>(p, c);
 
-    // ---- Q fragments of the QK heads: lane holds Q[head][128 g + 8 ks .. + 7];
-    // ks 16, 17 from q_rope (dims 32 (ks - 16) + 8 g).
+    // ---- Q fragments of the QK heads: lane holds Q[head][32 ks + 8
+    // qk_lane_chunk(g) .. + 7]; ks 16, 17 from q_rope (dims 32 (ks - 16) + 8 g).
     bf16x8 qf[18];
     {
         const int head = ghead0 + 16 * gw + n16;
-        const uint16_t* qrow = p.q + ((int64_t)c.token * p.H + head) * 512 + 128 * g;
+        const uint16_t* qrow = p.q + ((int64_t)c.token * p.H + head) * 512 + 8 * qk_lane_chunk(g);
 #pragma unroll
-        for (int ks = 0; ks < 16; ++ks) qf[ks] = *reinterpret_cast<const bf16x8*>(qrow + 8 * ks);
+        for (int ks = 0; ks < 16; ++ks) qf[ks] = *reinterpret_cast<const bf16x8*>(qrow + 32 * ks);
         const uint16_t* rrow = p.q_rope + ((int64_t)c.token * p.H + head) * 64 + 8 * g;
         qf[16] = *reinterpret_cast<const bf16x8*>(rrow);
         qf[17] = *reinterpret_cast<const bf16x8*>(rrow + 32);
@@ -2419,14 +2434,15 @@ __global__ __launch_bounds__(kPPThreads, 1) void sparse_mla_fwd_pp(FwdParams p) 
         asm volatile("" : "+v"(ln));
         const int lg = ln >> 4, ln16 = ln & 15;
         // K fragment of k-step ks, subtile s: row 16 s + n16, logical chunk
-        // 16 g + ks (kv) at byte 256 g + ((ks ^ sw_kv(n16)) << 4); rope chunk
-        // 4 (ks - 16) + g at ((4 (ks - 16) + g) ^ sw_rope(n16)) << 4.  Rows are
-        // 1 KiB (kv) / 128 B (rope) aligned, so the XORs act on a per-lane base.
-        const uint32_t kbase = (stage + ln16 * 1024 + ((uint32_t)lg << 8)) | ((uint32_t)sw_kv(ln16) << 4);
+        // 4 ks + qk_lane_chunk(g) (kv) at byte 256 (ks >> 2) + (((4 (ks & 3) +
+        // qk_lane_chunk(g)) ^ sw_kv(n16)) << 4); rope chunk 4 (ks - 16) + g at
+        // ((4 (ks - 16) + g) ^ sw_rope(n16)) << 4.  Rows are 1 KiB (kv) / 128 B
+        // (rope) aligned, so the XORs act on a per-lane base.
+        const uint32_t kbase = (stage + ln16 * 1024) | ((uint32_t)(qk_lane_chunk(lg) ^ sw_kv(ln16)) << 4);
         const uint32_t rbase = (stage + X::KV_BYTES + ln16 * 128) | ((uint32_t)(lg ^ sw_rope(ln16)) << 4);
         auto kfrag = [&](int step) -> bf16x8 {
             const int ks = step >> 1, sub = step & 1;
-            if (ks < 16) return lds_load<bf16x8>((kbase ^ (16u * ks)) + sub * 16 * 1024);
+            if (ks < 16) return lds_load<bf16x8>((kbase ^ (64u * (ks & 3))) + 256u * (ks >> 2) + sub * 16 * 1024);
             return lds_load<bf16x8>((rbase ^ (64u * (ks - 16))) + sub * 16 * 128);
         };
         constexpr int KD = PP_QK_DEPTH;
