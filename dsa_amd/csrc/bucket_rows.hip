@@ -67,15 +67,35 @@ __global__ __launch_bounds__(kThreads) void bucket_rows_kernel(const int32_t* __
         const int e = ((wave + 4 * r) << 6) + lane;
         const bool active = e < topk;
         const int b = (uint32_t)val[r] < kv_len ? (int)((uint32_t)val[r] >> shift) : kBuckets - 1;
-        uint64_t peers = ballot(active);
+        // 127 is no bucket: a lane past the row matches no active lane
+        const int key = active ? b : 127;
+        // This lane's peers (itself included) are the lanes whose key differs
+        // in no bit: per bit, the ballot of the bit XOR this lane's bit (0 or
+        // ~0), OR-ed into d with one three-input bitwise instruction per half
+        // (table 0xDE: d | (m ^ t); the last bit 0x21, its complement, so that
+        // d ends as the peers; both symmetric in the outer operands).  Four
+        // VALU instructions per bit, against ten for the select-and-AND form.
+        uint32_t plo = 0, phi = 0;
+        auto key_bit = [&](int bit, uint32_t& t) -> uint64_t {
+            t = (uint32_t)__builtin_amdgcn_sbfe(key, bit, 1);
+            asm volatile("" : "+v"(t));  // the ballot compares t itself (not a second shift of key)
+            return ballot(t != 0);
+        };
 #pragma unroll
-        for (int bit = 0; bit < 7; ++bit) {
-            const uint64_t m = ballot(active && ((b >> bit) & 1));
-            peers &= ((b >> bit) & 1) ? m : ~m;
+        for (int bit = 0; bit < 6; ++bit) {
+            uint32_t t;
+            const uint64_t m = key_bit(bit, t);
+            plo = __builtin_amdgcn_bitop3_b32((uint32_t)m, plo, t, 0xDE);
+            phi = __builtin_amdgcn_bitop3_b32((uint32_t)(m >> 32), phi, t, 0xDE);
         }
-        const int below = (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(peers >> 32),
-                                                         __builtin_amdgcn_mbcnt_lo((uint32_t)peers, 0u));
-        if (active && below == 0) counts[(wave + 4 * r) * kBuckets + b] = __popcll(peers);
+        {
+            uint32_t t;
+            const uint64_t m = key_bit(6, t);
+            plo = __builtin_amdgcn_bitop3_b32((uint32_t)m, plo, t, 0x21);
+            phi = __builtin_amdgcn_bitop3_b32((uint32_t)(m >> 32), phi, t, 0x21);
+        }
+        const int below = (int)__builtin_amdgcn_mbcnt_hi(phi, __builtin_amdgcn_mbcnt_lo(plo, 0u));
+        if (active && below == 0) counts[(wave + 4 * r) * kBuckets + b] = __popc(plo) + __popc(phi);
         bucket[r] = b;
         rank[r] = below;
     }
