@@ -1929,10 +1929,11 @@ __device__ __forceinline__ uint32_t pp_pchunk(int h, int g) {
 // kernel, or for 16 heads (arrival counters given) in the workgroup of each
 // (token, head group) that stores its partials last, as the column-split
 // kernel does (merge_if_last).
-// Fragment pipelines: 12 K reads (QK) and 6 V fragment pairs (PV) in flight
-// per wave; 8 / 5 and 14 / 7 measured the same.
+// Fragment pipelines: 10 K reads (QK) and 6 V fragment pairs (PV) in flight
+// per wave (with the k-order of qk_lane_chunk, 10 beat 8, 12 and 14 by
+// 0.4 % at C2; PV 4 and 8 measured the same as 6).
 #ifndef XS_QK_DEPTH
-#define XS_QK_DEPTH 12
+#define XS_QK_DEPTH 10
 #endif
 #ifndef XS_PV_DEPTH
 #define XS_PV_DEPTH 6
@@ -2324,8 +2325,10 @@ __global__ __launch_bounds__(64 * XsLds<HB>::WAVES, 1) void sparse_mla_fwd_xs(Fw
 // two-launch path only (no in-kernel merge).
 constexpr int kPPWaves = 8;
 constexpr int kPPThreads = 64 * kPPWaves;
+// K fragments in flight in the QK chain: 7 (with the k-order of
+// qk_lane_chunk, C5 -1 % against 6, 5 and 4; 8 spills)
 #ifndef PP_QK_DEPTH
-#define PP_QK_DEPTH 6
+#define PP_QK_DEPTH 7
 #endif
 
 struct PPLds {
