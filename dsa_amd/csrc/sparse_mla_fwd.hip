@@ -2430,19 +2430,43 @@ __global__ __launch_bounds__(kPPThreads, 1) void sparse_mla_fwd_pp(FwdParams p) 
     f32x4 oacc[4][8];  // [head block][column block]
     float m_ref = -FLT_MAX, m_true = -FLT_MAX, l_run = 0.f;
 
-    // QK + softmax of tile t for this wave's 16 heads; P to the group buffer.
-    auto qk_softmax = [&](int t, bool& overflow) __attribute__((always_inline)) {
-        const uint32_t stage = X::stage(lds, t);
-        int ln = lane;
-        asm volatile("" : "+v"(ln));
-        const int lg = ln >> 4, ln16 = ln & 15;
+    // This lane's LDS offsets in the tile loop, computed once and held in
+    // three registers (made opaque at every use, so that nothing derived from
+    // them is hoisted into more registers): off_kv = the K fragment base | the
+    // V^T base << 16, both relative to the stage; off_rope = the rope fragment
+    // base, relative to the stage; off_p = the P read offset (head block 0;
+    // block hb at + 1024 hb, since pp_pchunk's swizzle depends on (h >> 2) & 3
+    // = (n16 >> 2) & 3 only) | the P write offset << 16, in the group's P
+    // buffer.  Stages are 1 KiB aligned and each base's low bits hold its XOR
+    // terms, so stage + base equals the OR of the two.  (Recomputing them from
+    // the lane id every half-step took about 45 VALU instructions per tile.)
+    uint32_t off_kv, off_rope, off_p;
+    {
+        const int lg = lane >> 4, ln16 = lane & 15;
         // K fragment of k-step ks, subtile s: row 16 s + n16, logical chunk
         // 4 ks + qk_lane_chunk(g) (kv) at byte 256 (ks >> 2) + (((4 (ks & 3) +
         // qk_lane_chunk(g)) ^ sw_kv(n16)) << 4); rope chunk 4 (ks - 16) + g at
-        // ((4 (ks - 16) + g) ^ sw_rope(n16)) << 4.  Rows are 1 KiB (kv) / 128 B
-        // (rope) aligned, so the XORs act on a per-lane base.
-        const uint32_t kbase = (stage + ln16 * 1024) | ((uint32_t)(qk_lane_chunk(lg) ^ sw_kv(ln16)) << 4);
-        const uint32_t rbase = (stage + X::KV_BYTES + ln16 * 128) | ((uint32_t)(lg ^ sw_rope(ln16)) << 4);
+        // ((4 (ks - 16) + g) ^ sw_rope(n16)) << 4.
+        const uint32_t koff = (uint32_t)(ln16 * 1024) | ((uint32_t)(qk_lane_chunk(lg) ^ sw_kv(ln16)) << 4);
+        // V^T fragment of column block cb (columns 128 gw + 16 cb ..): transposed
+        // reads of rows 4 g + n16/4 and 16 + 4 g + n16/4 at column 4 (n16 & 3):
+        // logical chunk 16 gw + 2 cb + ((n16 & 3) >> 1), byte 8 (n16 & 1); the
+        // row is 1 KiB aligned and (2 cb + c) ^ sw = 2 cb ^ (c ^ sw) for c < 2.
+        const int tr_row = 4 * lg + (ln16 >> 2);
+        const uint32_t voff = (uint32_t)(tr_row * 1024 + (gw << 8)) +
+                              ((uint32_t)((((ln16 & 3) >> 1) ^ sw_kv(tr_row)) << 4) + ((ln16 & 1) << 3));
+        off_kv = koff | (voff << 16);
+        off_rope = (uint32_t)(X::KV_BYTES + ln16 * 128) | ((uint32_t)(lg ^ sw_rope(ln16)) << 4);
+        off_p = pp_pchunk(ln16, lg) | (pp_pchunk(16 * gw + ln16, lg) << 16);
+    }
+    static_assert(X::KV_BYTES + 16 * 128 <= 0xffff && 32 * 1024 <= 0xffff, "offsets fit 16 bits");
+
+    // QK + softmax of tile t for this wave's 16 heads; P to the group buffer.
+    auto qk_softmax = [&](int t, bool& overflow) __attribute__((always_inline)) {
+        const uint32_t stage = X::stage(lds, t);
+        asm volatile("" : "+v"(off_kv), "+v"(off_rope), "+v"(off_p));
+        const uint32_t kbase = stage + (off_kv & 0xffffu);
+        const uint32_t rbase = stage + off_rope;
         auto kfrag = [&](int step) -> bf16x8 {
             const int ks = step >> 1, sub = step & 1;
             if (ks < 16) return lds_load<bf16x8>((kbase ^ (64u * (ks & 3))) + 256u * (ks >> 2) + sub * 16 * 1024);
@@ -2471,6 +2495,9 @@ __global__ __launch_bounds__(kPPThreads, 1) void sparse_mla_fwd_pp(FwdParams p) 
 #pragma unroll
         for (int r = 0; r < 8; ++r) x[r] = sacc[r >> 2][r & 3];
         if (t == nt - 1) {
+            int ln = lane;
+            asm volatile("" : "+v"(ln));
+            const int lg = ln >> 4;
 #pragma unroll
             for (int sub = 0; sub < 2; ++sub) {
                 const i32x4 iv = lds_load<i32x4>(idx_lds + 4 * (t * BN + 16 * sub + 4 * lg));
@@ -2506,26 +2533,18 @@ __global__ __launch_bounds__(kPPThreads, 1) void sparse_mla_fwd_pp(FwdParams p) 
             }
         }
         l_run += psum;
-        lds_store<bf16x8>(p_lds + pp_pchunk(16 * gw + ln16, lg), pk);
+        lds_store<bf16x8>(p_lds + (off_p >> 16), pk);
     };
 
     // PV of tile t: O[head block hb][column block cb] += V^T . P^T over the
     // tile's 32 rows (one 16x16x32 MFMA per block pair).
     auto pv = [&](int t) __attribute__((always_inline)) {
         const uint32_t stage = X::stage(lds, t);
-        int ln = lane;
-        asm volatile("" : "+v"(ln));
-        const int lg = ln >> 4, ln16 = ln & 15;
+        asm volatile("" : "+v"(off_kv), "+v"(off_p));
         bf16x8 pf[4];
 #pragma unroll
-        for (int hb = 0; hb < 4; ++hb) pf[hb] = lds_load<bf16x8>(p_lds + pp_pchunk(16 * hb + ln16, lg));
-        // V^T fragment of column block cb (columns 128 gw + 16 cb ..): transposed
-        // reads of rows 4 g + n16/4 and 16 + 4 g + n16/4 at column 4 (n16 & 3):
-        // logical chunk 16 gw + 2 cb + ((n16 & 3) >> 1), byte 8 (n16 & 1); the
-        // row is 1 KiB aligned and (2 cb + c) ^ sw = 2 cb ^ (c ^ sw) for c < 2.
-        const int tr_row = 4 * lg + (ln16 >> 2);
-        const uint32_t vbase = (stage + tr_row * 1024 + ((uint32_t)gw << 8)) |
-                               ((uint32_t)((((ln16 & 3) >> 1) ^ sw_kv(tr_row)) << 4) + ((ln16 & 1) << 3));
+        for (int hb = 0; hb < 4; ++hb) pf[hb] = lds_load<bf16x8>(p_lds + (off_p & 0xffffu) + 1024 * hb);
+        const uint32_t vbase = stage + (off_kv >> 16);
         auto vfrag = [&](int cb) -> bf16x8 {
             const uint32_t a = vbase ^ (32u * cb);
             const bf16x4 v0 = lds_load_tr(a);
