@@ -2330,6 +2330,12 @@ constexpr int kPPThreads = 64 * kPPWaves;
 #ifndef PP_QK_DEPTH
 #define PP_QK_DEPTH 7
 #endif
+// Tiles whose gathers are issued before the prologue's full wait (for Q and
+// those tiles); the rest of the first three follow it.  1: the first QK
+// waits for tile 0 only (C5 -0.2 % against 3, same bits).
+#ifndef PP_PRE_TILES
+#define PP_PRE_TILES 1
+#endif
 
 struct PPLds {
     static constexpr int BN = 32, NSTAGE = 4;
@@ -2576,10 +2582,16 @@ __global__ __launch_bounds__(kPPThreads, 1) void sparse_mla_fwd_pp(FwdParams p) 
         bool overflow = false;
         if (grp == 0)
 #pragma unroll
-            for (int i = 0; i < 3; ++i)
+            for (int i = 0; i < PP_PRE_TILES; ++i)
                 if (i < nt) pp_issue(p, gt, i, X::stage(lds, i), idx_lds, gw, lane);
-        // Q (and the first tiles) complete here; see the wide variant.
+        // Q and the first PP_PRE_TILES tiles complete here (a full wait: the
+        // compiler does not count the gathers, see the wide variant); the
+        // loop's own waits cover the tiles issued after it.
         wait_vmcnt<0>();
+        if (grp == 0)
+#pragma unroll
+            for (int i = PP_PRE_TILES; i < 3; ++i)
+                if (i < nt) pp_issue(p, gt, i, X::stage(lds, i), idx_lds, gw, lane);
 
         // Half 2t starts when group 0's gathers of tile t have landed (tiles up
         // to t + 2 issued) and every wave is past half 2t - 1; in half 2t + 1
