@@ -128,9 +128,13 @@ PLANS_H128 = [Tuning(128, 32, 1, stages=4), Tuning(128, 32, 3, stages=4), Tuning
               Tuning(16, 64, 1, kv_waves=4, mfma=16, pv_cols=128), Tuning(16, 64, 9, kv_waves=4, mfma=16, pv_cols=128),
               Tuning(32, 64, 1, kv_waves=4, mfma=16, pv_cols=128), Tuning(32, 64, 5, kv_waves=4, mfma=16, pv_cols=128),
               Tuning(64, 64, 2, kv_waves=4, mfma=16, pv_cols=128), Tuning(64, 64, 7, kv_waves=4, mfma=16, pv_cols=128),
-              # ping-pong (128 heads, eight waves): one tile, three and 64 splits
+              # ping-pong (128 heads, eight waves): 1, 3, 16, 32 and 64 splits (with the
+              # invalid family's compaction, workgroups of 1 to 4 tiles at 16-64 splits:
+              # the prologue's first-tile wait and the ring's fill at every depth)
               Tuning(128, 32, 1, kv_waves=1, stages=4, mfma=16, pv_cols=128),
               Tuning(128, 32, 3, kv_waves=1, stages=4, mfma=16, pv_cols=128),
+              Tuning(128, 32, 16, kv_waves=1, stages=4, mfma=16, pv_cols=128),
+              Tuning(128, 32, 32, kv_waves=1, stages=4, mfma=16, pv_cols=128),
               Tuning(128, 32, 64, kv_waves=1, stages=4, mfma=16, pv_cols=128),
               # specialised waves (16 or 32 heads, 32-row tiles, gather waves)
               Tuning(16, 32, 1, kv_waves=2, stages=4, mfma=16, pv_cols=128),
